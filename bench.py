@@ -1,0 +1,214 @@
+"""Benchmark of the KV-cache hot path on one MI355X.
+
+A step is one engine decode step's worth of hot-path work for the GQA decode
+workload (64 rows, ctx U[128, 2048], 32/8 heads, D=128, bf16, block 16, pool
+1.25x shuffled): for each of 32 layers, the 64-token KV append
+(kvhot_reshape_and_cache) and the split-K paged decode attention
+(kvhot_paged_attention) over that layer's pool.  Each layer has its own
+~348 MB pool (11 GB in all), so a layer's K/V is never still resident in the
+256 MB Infinity Cache when it is read again.
+
+value = algorithmic bytes moved per step (K/V read + Q in + O out + block
+table + LSE out, plus the append's K/V read+write and slots) / step time, in
+GB/s (1e9).  roofline = the attention kernel alone: the same algorithmic bytes
+of one launch over its average duration, timed with HIP events on the launch
+stream across a run of back-to-back launches.  cpu_baseline = the reference's
+eager PyTorch path (restated in oracle/eager.py) on this host's cores, on one
+layer of the same batch.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload 2]
+"""
+from __future__ import annotations
+
+import argparse
+import importlib
+import json
+import math
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+
+
+def parse():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--workload", type=int, default=2, choices=[2, 3, 4, 5])
+    ap.add_argument("--layers", type=int, default=32)
+    ap.add_argument("--partition-tokens", type=int, default=0)
+    ap.add_argument("--kernel-reps", type=int, default=10, help="passes over all layers for the kernel timing")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=20.0, help="budget for the CPU baseline sample")
+    return ap.parse_args()
+
+
+def main():
+    args = parse()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); this build has no "
+              "multi-GPU path", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    sea = importlib.import_module("serving-engine_amd")
+    wl = importlib.import_module("serving-engine_amd.workloads")
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+
+    w = wl.make_workload(args.workload)
+    layers = args.layers if args.workload != 5 else 1  # the 40 GB pool is one layer's
+    t = wl.make_tensors(w, dev, num_layers=layers)
+    cache = sea._PagedKVCache(t.kv_cache)
+    meta = sea.build_paged_batch_metadata(w.scheduler_output(), device=dev)
+    slots = meta["slot_mapping"]
+    scale = 1.0 / math.sqrt(w.head_dim)
+    pt = args.partition_tokens or w.partition_tokens or None
+    blocks = [cache.blocks(i) for i in range(layers)]
+
+    def attention(i):
+        return sea.paged_flash_attention(t.q, blocks[i][0], blocks[i][1], meta, w.num_q_heads,
+                                         w.num_kv_heads, scale, partition_tokens=pt)
+
+    def step():
+        for i in range(layers):
+            cache.write(t.new_k, t.new_v, i, slots)
+            attention(i)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    for _ in range(args.steps):
+        step()
+    end.record()
+    torch.cuda.synchronize()
+    ms_per_step = start.elapsed_time(end) / args.steps
+
+    attn_bytes = w.decode_algorithmic_bytes()
+    append_bytes = w.append_bytes()
+    step_bytes = layers * (attn_bytes + append_bytes)
+    value = step_bytes / (ms_per_step * 1e-3) / 1e9
+
+    # Attention kernel alone: back-to-back launches over the layers.
+    reps = max(1, args.kernel_reps)
+    torch.cuda.synchronize()
+    start.record()
+    for _ in range(reps):
+        for i in range(layers):
+            attention(i)
+    end.record()
+    torch.cuda.synchronize()
+    attn_us = start.elapsed_time(end) * 1e3 / (reps * layers)
+    attn_gbs = attn_bytes / (attn_us * 1e-6) / 1e9
+
+    # Append alone.
+    torch.cuda.synchronize()
+    start.record()
+    for _ in range(reps):
+        for i in range(layers):
+            cache.write(t.new_k, t.new_v, i, slots)
+    end.record()
+    torch.cuda.synchronize()
+    append_us = start.elapsed_time(end) * 1e3 / (reps * layers)
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline(w, t, layer=0, budget_s=args.cpu_seconds, attn_bytes=attn_bytes + append_bytes)
+
+    line = {
+        "metric": "decode paged-attn HBM GB/s (% of 8 TB/s); engine output tokens/sec",
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16" if w.dtype == torch.bfloat16 else str(w.dtype).replace("torch.", ""),
+        "data": "synthetic",
+        "config": {
+            "workload": w.name,
+            "layers_per_step": layers,
+            "rows": len(w.rows),
+            "total_context_tokens": int(sum(x.k_len for x in w.rows)),
+            "block_size": w.block_size,
+            "pool_blocks_per_layer": w.num_blocks,
+            "append_tokens": w.total_query,
+            "partition_tokens": pt or "auto",
+            "seed": w.seed,
+        },
+        "pct_of_hbm_peak": round(100.0 * value / HBM_PEAK_GBS, 2),
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "attn_mfma_kernel (split-K decode, fused partition merge)",
+            "achieved": round(attn_gbs, 2),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(attn_gbs / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "algorithmic_bytes_per_launch": attn_bytes,
+            "avg_launch_us": round(attn_us, 3),
+        },
+        "append": {"avg_launch_us": round(append_us, 3), "algorithmic_bytes": append_bytes,
+                   "gbs": round(append_bytes / (append_us * 1e-6) / 1e9, 2)},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+def cpu_baseline(w, t, layer, budget_s, attn_bytes):
+    """The reference's eager path (oracle/eager.py) on this host: append +
+    dense masked attention for one layer of the same batch, same values."""
+    import torch
+
+    from oracle import eager
+
+    threads = torch.get_num_threads()
+    q = t.q.cpu()
+    nk = t.new_k.transpose(1, 2).squeeze(0).cpu()
+    nv = t.new_v.transpose(1, 2).squeeze(0).cpu()
+    kc0 = t.kv_cache[layer, 0].cpu()
+    vc0 = t.kv_cache[layer, 1].cpu()
+    slots = t.slot_mapping.cpu()
+    rows = eager.workload_rows(w)
+    est = len(w.rows) * w.num_q_heads * sum(x.k_len for x in w.rows) * 4
+    per_row = est > 2e9  # whole-batch scores would not fit comfortably
+    scale = 1.0 / math.sqrt(w.head_dim)
+
+    def once():
+        kc, vc = kc0.clone(), vc0.clone()
+        t0 = time.perf_counter()
+        eager.eager_step(q, nk, nv, kc, vc, slots, rows, scale, w.num_kv_heads, per_row=per_row)
+        return time.perf_counter() - t0
+
+    first = once()  # warm-up
+    reps = int(max(1, min(10, (budget_s - first) / max(first, 1e-3))))
+    times = [once() for _ in range(reps)]
+    sec = statistics.median(times)
+    return {
+        "value": round(attn_bytes / sec / 1e9, 3),
+        "unit": "GB/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"one layer of the same batch (append + {'per-row' if per_row else 'whole-batch'} dense "
+                  f"masked eager attention, bf16, torch CPU), median of {reps} reps after 1 warm-up; "
+                  f"{sec * 1e3:.1f} ms per layer",
+        "ms_per_layer": round(sec * 1e3, 2),
+    }
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,173 @@
+"""KV-cache owner and attention adapter: the hot-path half of the reference's
+serving_engine/model_runner.py, running on libkvhot.
+
+* ``_PagedKVCache(kv_cache)`` with ``write`` / ``update`` / ``blocks``
+  (serving_engine/model_runner.py:11-45) plus ``copy_blocks`` for
+  copy-on-write (no counterpart in the reference).
+* ``hip_paged_attention_forward``: the HF attention-interface function, same
+  contract as ``triton_paged_attention_forward``
+  (serving_engine/model_runner.py:48-59); ``register_attention()`` registers
+  it under ``PAGED_HIP_ATTN_IMPL`` (the reference registers its Triton adapter
+  at import, :62; here registration is explicit so importing this module
+  does not import transformers).
+* ``allocate_kv_cache`` / ``num_blocks_for_memory``: the pool of
+  serving_engine/model_runner.py:101-125.
+
+Model loading, tokenisation and sampling stay with the caller.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+from .block import BLOCK_SIZE
+from .paged_attention_kernel import build_paged_batch_metadata, paged_flash_attention
+
+PAGED_HIP_ATTN_IMPL = "paged|hip"
+
+
+class _PagedKVCache:
+    """Duck-typed cache object over the whole pool
+    kv_cache[num_layers, 2, num_blocks, block_size, num_kv_heads, head_dim]."""
+
+    def __init__(self, kv_cache: torch.Tensor):
+        if kv_cache.dim() != 6 or kv_cache.shape[1] != 2:
+            raise ValueError("kv_cache must be [num_layers, 2, num_blocks, block_size, num_kv_heads, head_dim]")
+        self.kv_cache = kv_cache
+        self.num_kv_heads = kv_cache.shape[-2]
+        self.head_dim = kv_cache.shape[-1]
+
+    def write(self, key_states, value_states, layer_idx, write_index):
+        """Scatter new K/V into their slots: k_cache.view(-1, Hkv, D)[write_index[i]] =
+        key_states[0, :, i, :] (serving_engine/model_runner.py:21-32), as one
+        kvhot_reshape_and_cache launch for K and V.  key_states/value_states:
+        [1, Hkv, S, D]; write_index: int64 (or int32) [S] on the cache device.
+        Slots outside the pool are skipped instead of raising."""
+        key = key_states.transpose(1, 2).squeeze(0)  # [S, Hkv, D] view, no copy
+        value = value_states.transpose(1, 2).squeeze(0)
+        k_cache = self.kv_cache[layer_idx, 0]
+        v_cache = self.kv_cache[layer_idx, 1]
+        if key.dim() != 3 or key.shape != value.shape:
+            raise ValueError(f"key {tuple(key_states.shape)} / value {tuple(value_states.shape)} must be [1, Hkv, S, D]")
+        s, hkv, d = key.shape
+        if hkv != self.num_kv_heads or d != self.head_dim:
+            raise ValueError(f"key/value heads/dim {hkv}/{d} do not match the cache {self.num_kv_heads}/{self.head_dim}")
+        if key.dtype != k_cache.dtype or value.dtype != v_cache.dtype:
+            raise TypeError(f"key/value dtype {key.dtype} does not match the cache dtype {k_cache.dtype}")
+        if write_index.dim() != 1 or write_index.shape[0] != s:
+            raise ValueError(f"write_index must be [{s}], got {tuple(write_index.shape)}")
+        if write_index.dtype not in (torch.int64, torch.int32):
+            raise TypeError(f"write_index must be int64 or int32, got {write_index.dtype}")
+        dev = k_cache.device
+        if key.device != dev or value.device != dev or write_index.device != dev:
+            raise ValueError("key, value, write_index and the cache must be on one GPU")
+        if s == 0:
+            return
+        write_index = write_index.contiguous()
+        lib = _lib.load()
+        status = lib.kvhot_reshape_and_cache(
+            key.data_ptr(), _lib.i64_array(key.stride()),
+            value.data_ptr(), _lib.i64_array(value.stride()),
+            k_cache.data_ptr(), _lib.i64_array(k_cache.stride()),
+            v_cache.data_ptr(), _lib.i64_array(v_cache.stride()),
+            write_index.data_ptr(), 1 if write_index.dtype == torch.int64 else 0,
+            s, hkv, d, k_cache.shape[1], k_cache.shape[0],
+            _lib.dtype_code(k_cache.dtype), _lib.stream_handle(dev))
+        _lib.check(status, "kvhot_reshape_and_cache")
+
+    def update(self, key_states, value_states, layer_idx, read_index, write_index):
+        """Eager path: write, then gather a dense [len(read_index), Hkv, D]
+        read tensor (serving_engine/model_runner.py:34-40).  Only the write is
+        on the hot path; the gather serves the dense eager attention."""
+        self.write(key_states, value_states, layer_idx, write_index)
+        k_cache = self.kv_cache[layer_idx, 0].view(-1, self.num_kv_heads, self.head_dim)
+        v_cache = self.kv_cache[layer_idx, 1].view(-1, self.num_kv_heads, self.head_dim)
+        return torch.index_select(k_cache, 0, read_index), torch.index_select(v_cache, 0, read_index)
+
+    def blocks(self, layer_idx):
+        """This layer's block-structured K and V, [num_blocks, block_size, Hkv, D]
+        each (serving_engine/model_runner.py:42-45)."""
+        return self.kv_cache[layer_idx, 0], self.kv_cache[layer_idx, 1]
+
+    def copy_blocks(self, src_block_ids, dst_block_ids):
+        """Copy-on-write data mover: kv_cache[:, :, dst[i]] = kv_cache[:, :, src[i]]
+        for every layer, K and V, in one launch.  Destinations must be unique
+        and disjoint from the sources (checked when the ids are host data)."""
+        src = torch.as_tensor(src_block_ids, dtype=torch.int64)
+        dst = torch.as_tensor(dst_block_ids, dtype=torch.int64)
+        if src.shape != dst.shape or src.dim() != 1:
+            raise ValueError("src_block_ids and dst_block_ids must be 1-D of equal length")
+        n = self.kv_cache.shape[2]
+        if src.device.type == "cpu" and dst.device.type == "cpu" and src.numel():
+            if int(src.min()) < 0 or int(src.max()) >= n or int(dst.min()) < 0 or int(dst.max()) >= n:
+                raise IndexError(f"block id out of range [0, {n})")
+            d = set(dst.tolist())
+            if len(d) != dst.numel():
+                raise ValueError("destination block ids must be unique")
+            if d & set(src.tolist()):
+                raise ValueError("a destination block is also a source block")
+        if src.numel() == 0:
+            return
+        dev = self.kv_cache.device
+        src = src.to(dev, non_blocking=True).contiguous()
+        dst = dst.to(dev, non_blocking=True).contiguous()
+        kv = self.kv_cache
+        es = kv.element_size()
+        block_bytes = kv[0, 0, 0].numel() * es
+        if not kv[0, 0, 0].is_contiguous():
+            raise ValueError("each block's [block_size, Hkv, D] payload must be contiguous")
+        lib = _lib.load()
+        status = lib.kvhot_copy_blocks(
+            kv.data_ptr(), kv.shape[0], kv.stride(0) * es, kv.stride(1) * es,
+            kv.stride(2) * es, block_bytes, n, src.data_ptr(), dst.data_ptr(),
+            src.numel(), _lib.stream_handle(dev))
+        _lib.check(status, "kvhot_copy_blocks")
+
+
+def hip_paged_attention_forward(module, query, key, value, attention_mask, scaling, **kwargs):
+    """HF attention-interface function (serving_engine/model_runner.py:48-59):
+    append this layer's K/V, then paged attention over the block pool.
+    query [1, Hq, S, D], key/value [1, Hkv, S, D]; kwargs cache, write_index,
+    paged_metadata.  Returns ([1, S, Hq, D], None)."""
+    cache: _PagedKVCache = kwargs["cache"]
+    cache.write(key, value, module.layer_idx, kwargs["write_index"])
+    k_cache_blocks, v_cache_blocks = cache.blocks(module.layer_idx)
+    q = query.transpose(1, 2).squeeze(0)  # [S, Hq, D]
+    o, _ = paged_flash_attention(
+        q, k_cache_blocks, v_cache_blocks, kwargs["paged_metadata"],
+        num_q_heads=q.shape[1], num_kv_heads=cache.num_kv_heads,
+        scale=scaling, is_causal=True,
+    )
+    return o.unsqueeze(0), None
+
+
+def register_attention(name: str = PAGED_HIP_ATTN_IMPL) -> str:
+    """Registers hip_paged_attention_forward in transformers' attention
+    registry (AttentionInterface.register) and returns the name."""
+    from transformers import AttentionInterface
+
+    AttentionInterface.register(name, hip_paged_attention_forward)
+    return name
+
+
+def allocate_kv_cache(num_layers, num_blocks, num_kv_heads, head_dim, dtype=torch.bfloat16,
+                      device="cuda", block_size=BLOCK_SIZE):
+    """Zero-filled pool [L, 2, N, block_size, Hkv, D] (serving_engine/model_runner.py:101-110)."""
+    return torch.zeros(num_layers, 2, num_blocks, block_size, num_kv_heads, head_dim,
+                       dtype=dtype, device=device)
+
+
+def num_blocks_for_memory(free_bytes, num_layers, num_kv_heads, head_dim, dtype=torch.bfloat16,
+                          gpu_memory_utilization=0.9, block_size=BLOCK_SIZE):
+    """Pool size from free memory (serving_engine/model_runner.py:112-125)."""
+    es = torch.empty((), dtype=dtype).element_size()
+    per_block = 2 * num_layers * block_size * num_kv_heads * head_dim * es
+    return int(free_bytes * gpu_memory_utilization) // per_block
+
+
+def step_inputs(scheduler_output, device="cuda"):
+    """Per-step device inputs of ModelRunner.forward's paged path
+    (serving_engine/model_runner.py:142-184): the metadata dict, whose
+    ``slot_mapping`` is the write_index and ``positions`` the position ids."""
+    meta = build_paged_batch_metadata(scheduler_output, device=device)
+    return meta, meta.get("slot_mapping"), meta.get("positions")

@@ -1,0 +1,379 @@
+"""Parity of the HIP hot path (through the C ABI) with the CPU oracle.
+
+KV append, block copy and slot mapping: bit-exact.  Attention: within
+atol 2e-2 / rtol 1e-2 for bf16/fp16 outputs and 1e-5 for fp32, against the
+fp64 oracle on identical seeded inputs; natural-log LSE within 2e-3 (16-bit)
+or 1e-5 (fp32).  Full-size workloads 1-5 run as generated; every case prints
+its name before touching the GPU.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import load_golden, sea_module
+from oracle import eager, paged_ref
+
+pytestmark = pytest.mark.gpu
+
+TOL = {
+    torch.bfloat16: dict(atol=2e-2, rtol=1e-2),
+    torch.float16: dict(atol=2e-2, rtol=1e-2),
+    torch.float32: dict(atol=1e-5, rtol=1e-5),
+}
+LSE_TOL = {
+    torch.bfloat16: dict(atol=2e-3, rtol=1e-4),
+    torch.float16: dict(atol=2e-3, rtol=1e-4),
+    torch.float32: dict(atol=1e-5, rtol=1e-5),
+}
+
+
+def announce(msg):
+    print(f"[gpu-case] {msg}", flush=True)
+
+
+def f32(t):
+    return t.float().cpu().numpy()
+
+
+def bits(t):
+    t = t.contiguous()
+    return t.view(torch.int16 if t.element_size() == 2 else torch.int32).cpu().numpy()
+
+
+@pytest.fixture(scope="module")
+def wl():
+    return sea_module("workloads")
+
+
+def oracle_step(w, T, rows=None):
+    """fp64 oracle of one step (append then attention) from the pre-step
+    tensors.  Only the blocks of the checked rows travel to the host: they are
+    gathered into a compact pool and the tables and slots are renumbered."""
+    q_lens, k_lens, q_starts, offs, bt = w.arrays()
+    rows = list(range(len(w.rows))) if rows is None else list(rows)
+    keep = np.zeros(len(q_lens), dtype=bool)
+    keep[rows] = True
+    need = [bt[r, : math.ceil(k_lens[r] / 16)] for r in rows if k_lens[r] > 0]
+    used = np.unique(np.concatenate(need)) if need else np.zeros(1, np.int64)
+    idx = torch.as_tensor(used, dtype=torch.int64, device=T.kv_cache.device)
+    kc = f32(T.kv_cache[0, 0].index_select(0, idx))
+    vc = f32(T.kv_cache[0, 1].index_select(0, idx))
+    slots = T.slot_mapping.cpu().numpy()
+    blk, off = slots // 16, slots % 16
+    pos = np.searchsorted(used, blk)
+    hit = (pos < len(used)) & (used[np.minimum(pos, len(used) - 1)] == blk)
+    new_slots = np.where(hit, pos * 16 + off, -1)
+    nk = f32(T.new_k.transpose(1, 2).squeeze(0))
+    nv = f32(T.new_v.transpose(1, 2).squeeze(0))
+    kc, vc = paged_ref.reshape_and_cache(kc, vc, nk, nv, new_slots)
+    bt_new = np.searchsorted(used, bt).clip(0, len(used) - 1).astype(np.int32)
+    return paged_ref.paged_attention(f32(T.q), kc, vc, np.where(keep, q_lens, 0), k_lens, q_starts, offs,
+                                     bt_new, w.num_q_heads, w.num_kv_heads, 1.0 / math.sqrt(w.head_dim))
+
+
+def hip_step(sea, wl, w, T, partition_tokens=None, meta=None):
+    cache = sea._PagedKVCache(T.kv_cache)
+    meta = meta if meta is not None else wl.metadata_tensors(w, T.q.device)
+    cache.write(T.new_k, T.new_v, 0, T.slot_mapping)
+    kc, vc = cache.blocks(0)
+    o, l = sea.paged_flash_attention(T.q, kc, vc, meta, w.num_q_heads, w.num_kv_heads,
+                                     1.0 / math.sqrt(w.head_dim), partition_tokens=partition_tokens)
+    torch.cuda.synchronize()
+    return o, l
+
+
+def assert_attention(w, o, l, ref_o, ref_lse, rows=None):
+    o_np, l_np = f32(o), l.cpu().numpy()
+    if rows is not None:
+        q_lens, _, q_starts, _, _ = w.arrays()
+        idx = np.concatenate([np.arange(q_starts[r], q_starts[r] + q_lens[r]) for r in rows])
+        o_np, l_np, ref_o, ref_lse = o_np[idx], l_np[idx], ref_o[idx], ref_lse[idx]
+    assert np.isfinite(o_np).all()
+    np.testing.assert_allclose(o_np, ref_o, **TOL[w.dtype])
+    np.testing.assert_allclose(l_np, ref_lse, **LSE_TOL[w.dtype])
+
+
+# ------------------------------------------------------------------ append --
+
+@pytest.mark.parametrize("config", [1, 2, 3])
+def test_append_bit_exact(cuda, sea, wl, config):
+    w = wl.make_workload(config)
+    announce(f"append workload {config}: {w.total_query} tokens")
+    T = wl.make_tensors(w, cuda)
+    kb, vb = bits(T.kv_cache[0, 0]), bits(T.kv_cache[0, 1])
+    nk = bits(T.new_k.transpose(1, 2).squeeze(0))
+    nv = bits(T.new_v.transpose(1, 2).squeeze(0))
+    sea._PagedKVCache(T.kv_cache).write(T.new_k, T.new_v, 0, T.slot_mapping)
+    torch.cuda.synchronize()
+    ek, ev = paged_ref.reshape_and_cache(kb, vb, nk, nv, T.slot_mapping.cpu().numpy())
+    assert np.array_equal(bits(T.kv_cache[0, 0]), ek)
+    assert np.array_equal(bits(T.kv_cache[0, 1]), ev)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32, torch.float16])
+def test_append_int32_slots_padding_and_strides(cuda, sea, dtype):
+    announce(f"append int32 slots / padding / strided source {dtype}")
+    g = torch.Generator(device=cuda).manual_seed(5)
+    kv = torch.randn(3, 2, 12, 16, 4, 64, generator=g, device=cuda).to(dtype)
+    src = torch.randn(4, 9, 64, generator=g, device=cuda).to(dtype)  # [Hkv, S, D] -> strided view
+    key = src.unsqueeze(0)           # [1, Hkv, S, D] with head stride S*D: a non-trivial view
+    val = (src * 2).unsqueeze(0)
+    slots = torch.tensor([5, -1, 191, 0, 12 * 16, 77, 100, -7, 130], dtype=torch.int32, device=cuda)
+    kb, vb = bits(kv[1, 0]), bits(kv[1, 1])
+    sea._PagedKVCache(kv).write(key, val, 1, slots)
+    torch.cuda.synchronize()
+    ek, ev = paged_ref.reshape_and_cache(kb, vb, bits(key[0].transpose(0, 1)), bits(val[0].transpose(0, 1)),
+                                         slots.cpu().numpy())
+    assert np.array_equal(bits(kv[1, 0]), ek)
+    assert np.array_equal(bits(kv[1, 1]), ev)
+
+
+# ------------------------------------------------------------- block copy --
+
+def test_copy_blocks_bit_exact(cuda, sea, wl):
+    w = wl.make_workload(4)
+    announce(f"copy_blocks {len(w.copy_src)} pairs x 2 layers")
+    kv = torch.empty(2, 2, w.num_blocks, 16, 8, 128, dtype=torch.bfloat16, device=cuda)
+    kv.view(torch.int16).random_(generator=torch.Generator(device=cuda).manual_seed(9))
+    before = bits(kv)
+    sea._PagedKVCache(kv).copy_blocks(w.copy_src, w.copy_dst)
+    torch.cuda.synchronize()
+    assert np.array_equal(bits(kv), paged_ref.copy_blocks(before, w.copy_src, w.copy_dst))
+
+
+def test_copy_blocks_rejects_overlap(sea):
+    kv = torch.zeros(1, 2, 8, 16, 1, 8)
+    with pytest.raises(ValueError):
+        sea._PagedKVCache(kv).copy_blocks([1, 2], [2, 3])
+
+
+# ---------------------------------------------------------- slot mapping --
+
+def test_metadata_and_slot_mapping_on_device(cuda, sea, wl):
+    w = wl.make_workload(3)
+    announce("build_paged_batch_metadata workload 3 on device")
+    so = w.scheduler_output()
+    meta = sea.build_paged_batch_metadata(so, device=cuda)
+    torch.cuda.synchronize()
+    rows = paged_ref.step_rows(so.scheduled_requests, so.prefill_chunk_sizes)
+    q_lens, k_lens, q_starts, offs, bt, mb, total = paged_ref.batch_metadata(rows)
+    assert meta["q_lens"].cpu().numpy().tolist() == q_lens.tolist()
+    assert meta["k_lens"].cpu().numpy().tolist() == k_lens.tolist()
+    assert meta["q_starts"].cpu().numpy().tolist() == q_starts.tolist()
+    assert meta["q_pos_offsets"].cpu().numpy().tolist() == offs.tolist()
+    assert np.array_equal(meta["block_table"].cpu().numpy(), bt)
+    assert meta["block_table_row_stride"] == mb and meta["total_query"] == total
+    slots, pos = paged_ref.write_slots_and_positions(rows, 16)
+    assert np.array_equal(meta["slot_mapping"].cpu().numpy(), slots)
+    assert np.array_equal(meta["positions"].cpu().numpy(), pos)
+    assert np.array_equal(slots, w.slot_mapping())
+
+
+# -------------------------------------------------------------- attention --
+
+@pytest.mark.parametrize("name", ["config1_fp32.npz", "gqa_bf16_mixed.npz"])
+def test_golden_fixture(cuda, sea, name):
+    g = load_golden(name)
+    announce(f"golden {name}")
+    kv = torch.stack([g["k_cache"], g["v_cache"]]).unsqueeze(0).to(cuda)
+    cache = sea._PagedKVCache(kv)
+    cache.write(g["new_k"].transpose(0, 1).unsqueeze(0).to(cuda), g["new_v"].transpose(0, 1).unsqueeze(0).to(cuda),
+                0, torch.from_numpy(g["slot_mapping"]).to(cuda))
+    meta = {k: torch.from_numpy(g[k]).to(cuda) for k in ("q_lens", "k_lens", "q_starts", "q_pos_offsets",
+                                                          "block_table")}
+    meta["block_table_row_stride"] = g["block_table"].shape[1]
+    kc, vc = cache.blocks(0)
+    o, l = sea.paged_flash_attention(g["q"].to(cuda), kc, vc, meta, g["num_q_heads"], g["num_kv_heads"],
+                                     1.0 / math.sqrt(g["head_dim"]))
+    torch.cuda.synchronize()
+    live = np.concatenate([np.arange(s, s + n) for s, n in zip(g["q_starts"], g["q_lens"])])
+    np.testing.assert_allclose(f32(o)[live], g["expected_o"][live], **TOL[g["dtype"]])
+    np.testing.assert_allclose(l.cpu().numpy()[live], g["expected_lse"][live], **LSE_TOL[g["dtype"]])
+
+
+def test_config1_fp32(cuda, sea, wl):
+    w = wl.make_workload(1)
+    announce("attention workload 1 (fp32)")
+    T = wl.make_tensors(w, cuda)
+    ref_o, ref_l = oracle_step(w, T)
+    o, l = hip_step(sea, wl, w, T)
+    assert_attention(w, o, l, ref_o, ref_l)
+
+
+@pytest.fixture(scope="module")
+def config2(cuda, wl):
+    w = wl.make_workload(2)
+    T = wl.make_tensors(w, cuda)
+    snapshot = T.kv_cache.clone()
+    ref = oracle_step(w, T)
+    return w, T, snapshot, ref
+
+
+def test_config2_decode(cuda, sea, wl, config2):
+    w, T, snap, (ref_o, ref_l) = config2
+    announce("attention workload 2 (bf16 GQA decode, 64 rows)")
+    T.kv_cache.copy_(snap)
+    o, l = hip_step(sea, wl, w, T)
+    assert_attention(w, o, l, ref_o, ref_l)
+    # same step again: the split-K counters left the workspace clean
+    T.kv_cache.copy_(snap)
+    o2, l2 = hip_step(sea, wl, w, T)
+    assert torch.equal(o, o2) and torch.equal(l, l2)
+
+
+def test_config2_matches_eager_restatement(cuda, sea, wl, config2):
+    """Against the reference's own eager path restated in torch-CPU bf16."""
+    w, T, snap, _ = config2
+    announce("attention workload 2 vs torch-CPU eager path")
+    T.kv_cache.copy_(snap)
+    o, _ = hip_step(sea, wl, w, T)
+    o_eager = eager.eager_step(T.q.cpu(), T.new_k.transpose(1, 2).squeeze(0).cpu(),
+                               T.new_v.transpose(1, 2).squeeze(0).cpu(), snap[0, 0].cpu(), snap[0, 1].cpu(),
+                               T.slot_mapping.cpu(), eager.workload_rows(w), 1.0 / math.sqrt(128), 8)
+    np.testing.assert_allclose(f32(o), o_eager.float().numpy(), **TOL[torch.bfloat16])
+
+
+@pytest.mark.parametrize("pt", [32, 64, 128, 256, 512, 1024])
+def test_config2_partition_sizes(cuda, sea, wl, config2, pt):
+    w, T, snap, (ref_o, ref_l) = config2
+    announce(f"attention workload 2, split-K partition {pt}")
+    T.kv_cache.copy_(snap)
+    o, l = hip_step(sea, wl, w, T, partition_tokens=pt)
+    assert_attention(w, o, l, ref_o, ref_l)
+
+
+def test_config3_mixed_prefill_decode(cuda, sea, wl):
+    w = wl.make_workload(3)
+    announce("attention workload 3 (8 x 512-token chunks + 56 decode rows)")
+    T = wl.make_tensors(w, cuda)
+    ref_o, ref_l = oracle_step(w, T)
+    o, l = hip_step(sea, wl, w, T, meta=sea.build_paged_batch_metadata(w.scheduler_output(), device=cuda))
+    assert_attention(w, o, l, ref_o, ref_l)
+
+
+def test_config4_prefix_sharing_and_cow(cuda, sea, wl):
+    w = wl.make_workload(4)
+    announce("attention workload 4 (256 rows sharing 64 blocks) + copy-on-write")
+    T = wl.make_tensors(w, cuda)
+    ref_o, ref_l = oracle_step(w, T)
+    o, l = hip_step(sea, wl, w, T)
+    assert_attention(w, o, l, ref_o, ref_l)
+    # copy-on-write: move every row's last block to a fresh copy and re-point the table
+    cache = sea._PagedKVCache(T.kv_cache)
+    cache.copy_blocks(w.copy_src, w.copy_dst)
+    meta = wl.metadata_tensors(w, cuda)
+    bt = meta["block_table"]
+    for i, x in enumerate(w.rows):
+        bt[i, math.ceil(x.k_len / 16) - 1] = int(w.copy_dst[i])
+    kc, vc = cache.blocks(0)
+    o2, l2 = sea.paged_flash_attention(T.q, kc, vc, meta, 32, 8, 1.0 / math.sqrt(128))
+    torch.cuda.synchronize()
+    assert torch.equal(o, o2) and torch.equal(l, l2)
+
+
+def test_config5_long_context_40gb_pool(cuda, sea, wl):
+    w = wl.make_workload(5)
+    announce("attention workload 5 (16 x 32768 tokens, 40 GB pool)")
+    T = wl.make_tensors(w, cuda)
+    rows = [0, 11]
+    ref_o, ref_l = oracle_step(w, T, rows=rows)
+    o, l = hip_step(sea, wl, w, T, partition_tokens=512)
+    assert int(w.used_blocks().max()) * 16 * 8 * 128 >= 2**31  # offsets need 64 bits
+    assert_attention(w, o, l, ref_o, ref_l, rows=rows)
+    assert torch.isfinite(o.float()).all() and torch.isfinite(l).all()
+
+
+# -------------------------------------------------------- shape coverage --
+
+def custom(wl, spec, hq, hkv, d, dtype, seed=3):
+    """spec: (q_len, k_len, q_pos_offset) rows over a shuffled pool."""
+    rng = np.random.default_rng(seed)
+    need = [max(1, math.ceil(k / 16)) for _, k, _ in spec]
+    n = sum(need) + 7
+    perm = rng.permutation(n)
+    rows, k0 = [], 0
+    for (ql, kl, off), nb in zip(spec, need):
+        rows.append(wl.Row(ql, kl, off, perm[k0:k0 + nb].astype(np.int64), ql != 1))
+        k0 += nb
+    return wl.Workload(0, "custom", dtype, hq, hkv, d, n, 1.0, rows, seed=seed)
+
+
+MIXED = [(1, 17, 16), (20, 50, 30), (1, 1, 0), (0, 16, 16), (3, 3, 0), (1, 33, 32), (40, 40, 0),
+         (1, 700, 699), (9, 300, 291)]
+
+SHAPES = [
+    (32, 8, 128, torch.bfloat16), (8, 8, 128, torch.bfloat16), (16, 8, 128, torch.bfloat16),
+    (64, 8, 128, torch.bfloat16), (32, 2, 128, torch.bfloat16), (32, 8, 64, torch.bfloat16),
+    (16, 4, 256, torch.bfloat16), (32, 8, 128, torch.float16), (12, 4, 96, torch.bfloat16),
+    (32, 8, 128, torch.float32), (12, 12, 64, torch.float32), (24, 8, 128, torch.bfloat16),
+]
+
+
+@pytest.mark.parametrize("hq,hkv,d,dtype", SHAPES)
+def test_shapes_mixed_batch(cuda, sea, wl, hq, hkv, d, dtype):
+    w = custom(wl, MIXED, hq, hkv, d, dtype)
+    announce(f"mixed batch Hq={hq} Hkv={hkv} D={d} {dtype}")
+    T = wl.make_tensors(w, cuda)
+    ref_o, ref_l = oracle_step(w, T)
+    o, l = hip_step(sea, wl, w, T, partition_tokens=64)
+    live = [i for i, x in enumerate(w.rows) if x.q_len > 0]
+    assert_attention(w, o, l, ref_o, ref_l, rows=live)
+
+
+def test_non_causal(cuda, sea, wl):
+    w = custom(wl, [(5, 40, 0), (1, 100, 50), (33, 33, 0)], 32, 8, 128, torch.bfloat16)
+    announce("non-causal")
+    T = wl.make_tensors(w, cuda)
+    cache = sea._PagedKVCache(T.kv_cache)
+    cache.write(T.new_k, T.new_v, 0, T.slot_mapping)
+    kc, vc = cache.blocks(0)
+    o, l = sea.paged_flash_attention(T.q, kc, vc, wl.metadata_tensors(w, cuda), 32, 8,
+                                     1.0 / math.sqrt(128), is_causal=False, partition_tokens=32)
+    torch.cuda.synchronize()
+    kcn, vcn = f32(T.kv_cache[0, 0]), f32(T.kv_cache[0, 1])
+    q_lens, k_lens, q_starts, offs, bt = w.arrays()
+    ref_o, ref_l = paged_ref.paged_attention(f32(T.q), kcn, vcn, q_lens, k_lens, q_starts, offs, bt, 32, 8,
+                                             1.0 / math.sqrt(128), is_causal=False)
+    np.testing.assert_allclose(f32(o), ref_o, **TOL[torch.bfloat16])
+    np.testing.assert_allclose(l.cpu().numpy(), ref_l, **LSE_TOL[torch.bfloat16])
+
+
+def test_strided_query_and_empty_key_row(cuda, sea, wl):
+    w = custom(wl, [(1, 50, 49), (4, 20, 16), (1, 0, -1)], 32, 8, 128, torch.bfloat16)
+    announce("strided q view + row without keys")
+    T = wl.make_tensors(w, cuda)
+    # q as HF hands it over: [1, Hq, S, D] transposed view -> [S, Hq, D] non-contiguous
+    q_hsd = T.q.transpose(0, 1).contiguous()
+    q = q_hsd.transpose(0, 1)
+    assert not q.is_contiguous()
+    cache = sea._PagedKVCache(T.kv_cache)
+    kc, vc = cache.blocks(0)
+    o, l = sea.paged_flash_attention(q, kc, vc, wl.metadata_tensors(w, cuda), 32, 8, 1.0 / math.sqrt(128))
+    torch.cuda.synchronize()
+    assert o.stride() == q.stride()
+    q_lens, k_lens, q_starts, offs, bt = w.arrays()
+    ref_o, ref_l = paged_ref.paged_attention(f32(T.q), f32(T.kv_cache[0, 0]), f32(T.kv_cache[0, 1]),
+                                             q_lens, k_lens, q_starts, offs, bt, 32, 8, 1.0 / math.sqrt(128))
+    np.testing.assert_allclose(f32(o), ref_o, **TOL[torch.bfloat16])
+    assert (f32(o)[5] == 0).all() and np.isneginf(l.cpu().numpy()[5]).all()
+
+
+def test_hf_attention_adapter(cuda, sea, wl):
+    w = custom(wl, [(1, 70, 69), (12, 30, 18), (1, 17, 16)], 32, 8, 128, torch.bfloat16)
+    announce("HF attention adapter")
+    T = wl.make_tensors(w, cuda)
+    ref_o, ref_l = oracle_step(w, T)
+    meta = sea.build_paged_batch_metadata(w.scheduler_output(), device=cuda)
+
+    class Module:
+        layer_idx = 0
+
+    query = T.q.transpose(0, 1).unsqueeze(0)  # [1, Hq, S, D]
+    out, weights = sea.hip_paged_attention_forward(
+        Module(), query, T.new_k, T.new_v, None, 1.0 / math.sqrt(128),
+        cache=sea._PagedKVCache(T.kv_cache), write_index=meta["slot_mapping"], paged_metadata=meta)
+    torch.cuda.synchronize()
+    assert weights is None and out.shape == (1, w.total_query, 32, 128)
+    np.testing.assert_allclose(f32(out[0]), ref_o, **TOL[torch.bfloat16])
