@@ -132,6 +132,34 @@ int64_t kvhot_paged_attention_workspace_bytes(
     int64_t head_dim, int64_t block_size, int64_t partition_tokens, int dtype);
 
 /*
+ * Launch list ("schedule") for kvhot_paged_attention, built on the host from
+ * HOST copies of q_lens, k_lens, q_starts, q_pos_offsets and the block table,
+ * with the head counts, head_dim, block_size, is_causal and dtype the
+ * attention call will get.  Decode rows are cut into pieces of near-equal
+ * length, sized so that all decode waves fit on the current device at once,
+ * and packed into work-groups: num_decode_units per-wave descriptors (whole
+ * work-groups; each carries its row's metadata and first block so the wave's
+ * first K/V loads depend on nothing else), followed by num_prefill_units
+ * per-work-group prefill units, 8 int32 per unit, longest first.  partition_tokens = 0 lets the planner choose the key
+ * partition; the size it used is returned in *partition_tokens_used and must
+ * be passed as partition_tokens to kvhot_paged_attention (and to the
+ * workspace query).  Returns the total unit count (units are written when
+ * `units` is non-NULL and capacity_units suffices) or a negative KVHOT_E*
+ * code.  A schedule depends only on the step's lengths, so one upload serves
+ * every layer of an engine step.  Without a schedule the attention launch
+ * covers the padded grid of (row, partition, head group), and work-groups
+ * without work still cost a launch slot each.
+ */
+int64_t kvhot_paged_attention_schedule(
+    const int32_t* q_lens, const int32_t* k_lens, const int32_t* q_starts,
+    const int32_t* q_pos_offsets, const int32_t* block_table,
+    int64_t bt_row_stride, int64_t num_rows, int64_t num_q_heads, int64_t num_kv_heads,
+    int64_t head_dim, int64_t block_size, int64_t partition_tokens,
+    int is_causal, int dtype, int32_t* units, int64_t capacity_units,
+    int64_t* num_decode_units, int64_t* num_prefill_units,
+    int64_t* partition_tokens_used);
+
+/*
  * Paged attention forward over a ragged batch of rows (prefill chunks and
  * decode rows mixed), one call per layer.  For row r with n_q = q_lens[r],
  * n_k = k_lens[r], off = q_pos_offsets[r], and each query i < n_q (global
@@ -145,8 +173,9 @@ int64_t kvhot_paged_attention_workspace_bytes(
  * partition_tokens keys, then a merge launch when any row has more than one
  * partition); rows with n_q >= 2 run the chunked-prefill kernel.  max_q_len / max_k_len must bound
  * q_lens / k_lens (they size the grid; no device->host sync is made).
- * partition_tokens = 0 picks a size; otherwise a multiple of 32 in
- * [32, 64*block_size].
+ * partition_tokens (keys per decode work-group) = 0 picks a size; otherwise a
+ * multiple of 32 up to 2^20.  schedule: device copy of the units from
+ * kvhot_paged_attention_schedule for exactly these lengths and sizes, or NULL.
  * lse may be NULL.  out has the dtype of q, k_cache and v_cache; lse is fp32.
  * Replaces paged_flash_attention + paged_flash_fwd_kernel
  * (serving_engine/paged_attention_kernel.py:16-160).
@@ -163,8 +192,9 @@ int kvhot_paged_attention(
     int64_t max_q_len, int64_t max_k_len, int64_t num_q_heads,
     int64_t num_kv_heads, int64_t head_dim, int64_t block_size,
     int64_t num_blocks, float scale, int is_causal, int dtype,
-    int64_t partition_tokens, void* workspace, int64_t workspace_bytes,
-    void* stream);
+    int64_t partition_tokens, const int32_t* schedule,
+    int64_t num_decode_units, int64_t num_prefill_units, void* workspace,
+    int64_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

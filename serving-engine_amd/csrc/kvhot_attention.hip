@@ -1,32 +1,39 @@
 // Paged attention over a ragged batch of prefill chunks and decode rows.
 //
-// Kernel map (one wavefront per work-group throughout):
-//  * attn_mfma_kernel<T, D, NM>, bf16/f16.  A wave owns one (row, kv head,
-//    query block, key partition).  Its 16*NM "m-rows" are (query, head) pairs
-//    of one GQA group, so every K/V byte it loads serves all G = Hq/Hkv query
-//    heads of that kv head.  Keys are walked in tiles of 32 tokens (two
-//    16-token block slices).  Scores are formed transposed, S^T = K . Q^T, with
-//    v_mfma_f32_16x16x32: K rows (token-major, head_dim contiguous) are already
-//    the MFMA A-operand layout, so K goes HBM -> VGPR with no LDS round trip.
-//    The accumulator layout of S^T (lane = m-row, 4 tokens per lane) is exactly
-//    the B-operand layout P^T needs for O^T = V^T . P^T, so probabilities never
-//    leave registers.  V^T is formed in registers with v_perm_b32 from 16-byte
-//    row loads.  Softmax statistics live in the lane that owns the m-row, so
+// Kernel map:
+//  * WaveAttn<T, D, NM>: one wavefront attends 16*NM "m-rows" -- (query, head)
+//    pairs of one GQA group, so every K/V byte it loads serves all
+//    G = Hq/Hkv query heads of that kv head -- over a key range.  Keys are
+//    walked in 16-token block slices.  Scores are formed transposed,
+//    S^T = K . Q^T, with v_mfma_f32_16x16x32: K rows (token-major, head_dim
+//    contiguous) are already the MFMA A-operand layout, so K goes HBM -> VGPR
+//    with no LDS round trip.  The accumulator layout of S^T (lane = m-row,
+//    4 tokens per lane) is exactly the B-operand layout P^T needs for
+//    O^T = V^T . P^T on v_mfma_f32_16x16x16, so probabilities never leave
+//    registers.  V^T is formed in registers with v_perm_b32 from 16-byte row
+//    loads.  Softmax statistics live in the lane that owns the m-row, so
 //    rescaling O needs no cross-lane traffic.
-//    - decode launch (role 0, rows with q_len == 1, NM = 1): split-K over key
-//      partitions.  A row with one partition is finished in place; otherwise
-//      each partition stores (LSE, normalised O) with plain stores and
-//      attn_merge_kernel combines them in a second launch.  (Merging inside
-//      the first launch needs a device-scope release per wave, which on
-//      gfx950 is an L2 write-back per wave: far slower than a launch.)
-//    - prefill launch (role 1, rows with q_len >= 2, NM = 4): 16*4/G queries
-//      per wave, causal mask from q_pos_offset, tiles past the diagonal skipped.
+//  * attn_decode_kernel<T, D, W>: rows with q_len == 1.  Decode time is set by
+//    the longest chain of dependent slice loads in any wave, so a row's keys
+//    are split over S = 1, 2, 4 or 8 waves per kv head (about
+//    KVHOT_SLICES_PER_WAVE slices each); a work-group of W = 8 waves serves
+//    W/S kv heads of one row and merges each head's S pieces through LDS.
+//    Only a row longer than one key partition stores (LSE, O) partials to
+//    HBM, combined by attn_merge_kernel in a second launch.  (Merging across
+//    work-groups inside one launch needs a device-scope release per wave,
+//    which on gfx950 is an L2 write-back per wave -- far slower than a launch;
+//    partial stores interleaved with the K/V stream also cost bandwidth, so
+//    they are kept to long rows.)
+//  * attn_prefill_kernel<T, D, NM>: rows with q_len >= 2.  One wave per
+//    (row, kv head, block of 16*NM/G queries); causal mask from q_pos_offset;
+//    key tiles past the block's last query are never loaded.
 //  * attn_generic_kernel<T>: VALU kernel for fp32 (exact fp32 arithmetic) and
-//    for shapes the MFMA kernel does not cover.
+//    for shapes the MFMA kernels do not cover.
 #include "kvhot_internal.h"
 
 #include <algorithm>
 #include <climits>
+#include <vector>
 
 namespace kvhot {
 
@@ -54,12 +61,39 @@ struct AttnArgs {
   int32_t part_tokens, max_parts;
   float scale_log2;
   int32_t causal;
-  int32_t role;  // 0: rows with q_len == 1; 1: rows with q_len >= 2; 2: all rows
-  int32_t D;     // head_dim (generic kernel)
+  int32_t D;        // head_dim (generic kernel)
   int64_t total_q;  // rows of q / out / lse: outputs are only written below it
+  // Launch list from kvhot_paged_attention_schedule (decode: two int4 per wave,
+  // prefill: two int4 per work-group), or null: then the grid enumerates every
+  // (row, partition, head group) and work-groups without work exit.
+  const int4* sched;
 };
 
 __device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Buffer resource over [base, base + bytes): loads through it take a 32-bit
+// lane offset (no 64-bit per-lane address registers), and the hardware returns
+// zeros for any offset past `bytes`.  Word 3 = 0x00020000: raw dword access
+// for CDNA.
+__device__ inline __amdgpu_buffer_rsrc_t block_rsrc(const void* base, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, 0x00020000);
+}
+
+// Loads N dwords (N in {2, 4, 8}) at byte offset off (+ uniform soff) of r.
+template <int N>
+__device__ inline void buffer_dwords(__amdgpu_buffer_rsrc_t r, int off, int soff, uint32_t* out) {
+  if constexpr (N == 2) {
+    const u32x2 v = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(r, off, soff, 0));
+    out[0] = v.x; out[1] = v.y;
+  } else {
+#pragma unroll
+    for (int c = 0; c < N / 4; ++c) {
+      const u32x4 v = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off + 16 * c, soff, 0));
+      out[4 * c + 0] = v.x; out[4 * c + 1] = v.y;
+      out[4 * c + 2] = v.z; out[4 * c + 3] = v.w;
+    }
+  }
+}
 
 // Loads N dwords (N in {2, 4, 8}) from a 16-bit element pointer.
 template <int N>
@@ -78,301 +112,430 @@ __device__ inline void load_dwords(const uint16_t* p, uint32_t* out) {
 }
 
 template <int D>
-struct KVTile {
+struct KVSlice {
   static constexpr int NC = D / 32;   // 32-wide head_dim chunks of Q.K
-  static constexpr int VW = D / 32;   // dwords per V row slice per lane (D/16 elements)
-  u32x4 k[2][NC];                     // [slice][chunk]: token n, dims 8*(4c+g)..+8
-  uint32_t v[8][VW];                  // [k-slot]: token tok(g, slot), dims (D/16)*n..+D/16
+  static constexpr int VW = D / 32;   // dwords per V row per lane (D/16 elements)
+  u32x4 k[NC];                        // token n, dims 8*(4c+g)..+8
+  uint32_t v[4][VW];                  // token 4g+j, dims (D/16)*n..+D/16
 };
 
-// Which key token (0..31 within a tile) k-slot s8 of lane group g holds.
-__device__ inline int slot_token(int g, int s8) {
-  return (s8 < 4) ? (4 * g + s8) : (16 + 4 * g + (s8 - 4));
+// Key partition a decode row is cut into, shared by the split and merge
+// kernels: visible keys, clamped to what the grid and workspace were sized for.
+__device__ inline int decode_visible_keys(const AttnArgs& a, int row) {
+  const int klen = a.k_lens[row];
+  int kend = a.causal ? min(klen, a.q_offs[row] + 1) : klen;
+  kend = max(kend, 0);
+  return static_cast<int>(min(static_cast<int64_t>(kend),
+                              static_cast<int64_t>(a.max_parts) * a.part_tokens));
 }
 
+// One wavefront's attention state and key loop.
 template <class TT, int D, int NM, bool DB>
-__global__ void __launch_bounds__(64)
-attn_mfma_kernel(const AttnArgs a) {
-  constexpr int NC = D / 32;
-  constexpr int EPL = D / 16;   // head_dim values per lane per V row; PV MFMAs per tile
-  constexpr int VW = EPL / 2;
-  constexpr int MR = 16 * NM;   // m-rows per wave
+struct WaveAttn {
+  static constexpr int NC = D / 32;
+  static constexpr int EPL = D / 16;  // head_dim values per lane per V row; PV MFMAs per tile
+  static constexpr int VW = EPL / 2;
   using st = uint16_t;
 
-  const int lane = threadIdx.x;
-  const int n = lane & 15;
-  const int g = lane >> 4;
-  const int row = blockIdx.z;
-  const int qlen = a.q_lens[row];
-  if (a.role == 0 ? (qlen != 1) : (qlen < 2)) return;
-  const int kvh = blockIdx.x % a.Hkv;
-  const int qblk = blockIdx.x / a.Hkv;
-  const int G = a.G;
-  const int QPW = MR / G;
-  const int q0 = qblk * QPW;
-  if (q0 >= qlen) return;
-  const int nq = min(QPW, qlen - q0);
-  const int off = a.q_offs[row];
-  const int klen = a.k_lens[row];
-  int kend = a.causal ? min(klen, off + q0 + nq) : klen;
-  kend = max(kend, 0);
-  const int PT = a.part_tokens;
-  // Never more partitions than the grid and the workspace were sized for.
-  kend = static_cast<int>(min(static_cast<int64_t>(kend), static_cast<int64_t>(a.max_parts) * PT));
-  const int nparts = max((kend + PT - 1) / PT, 1);
-  const int p = blockIdx.y;
-  if (p >= nparts) return;
-  const int kbeg = p * PT;
-  const int kstop = min(kend, kbeg + PT);
-  const int qs = a.q_starts[row];
-
-  // ---- per-lane m-rows and Q (B operand of S^T = K . Q^T) ----
+  int n, g;
+  // m-row s*16 + n of this lane: query index (within the block), head, validity
   int mq[NM], mh[NM], qpos[NM];
   bool mval[NM];
-  u32x4 qf[NM][NC];
-#pragma unroll
-  for (int s = 0; s < NM; ++s) {
-    const int i = 16 * s + n;
-    mq[s] = i / G;
-    mh[s] = kvh * G + (i % G);
-    mval[s] = mq[s] < nq && static_cast<int64_t>(qs) + q0 + mq[s] < a.total_q;
-    qpos[s] = mval[s] ? (a.causal ? off + q0 + mq[s] : INT_MAX) : -1;
-#pragma unroll
-    for (int c = 0; c < NC; ++c) qf[s][c] = u32x4{0, 0, 0, 0};
-    if (mval[s]) {
-      const st* qp = static_cast<const st*>(a.q) +
-                     (static_cast<int64_t>(qs) + q0 + mq[s]) * a.q_st +
-                     static_cast<int64_t>(mh[s]) * a.q_sh;
-#pragma unroll
-      for (int c = 0; c < NC; ++c)
-        qf[s][c] = *reinterpret_cast<const u32x4*>(qp + 8 * (4 * c + g));
-    }
-  }
-  // Smallest query position of the wave: keys up to it are visible to all m-rows.
-  const int qpos_min = a.causal ? off + q0 : INT_MAX;
-
-  // ---- block table: lane j holds the id of logical block win + j, for a
-  // window of 64 blocks loaded once before its tiles are walked ----
-  const int bs = a.bs;
-  const int32_t* btrow = a.bt + static_cast<int64_t>(row) * a.bt_stride;
-  const int nb_row = min(static_cast<int64_t>((kstop + bs - 1) / bs), a.bt_stride);
-  int win = 0;
-  int bt_reg = 0;
-  auto block_of = [&](int lb) -> int64_t {
-    int64_t id = __builtin_amdgcn_readlane(bt_reg, lb - win);
-    id = id < 0 ? 0 : (id >= a.num_blocks ? a.num_blocks - 1 : id);
-    return id;
-  };
-
-  // Loop-invariant per-lane element offsets inside a 16-token block slice.
-  const int k_lane = n * static_cast<int>(a.k_st) + 8 * g;
-  int v_lane[4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) v_lane[j] = (4 * g + j) * static_cast<int>(a.v_st) + EPL * n;
-
-  const st* kbase = static_cast<const st*>(a.k) + static_cast<int64_t>(kvh) * a.k_sh;
-  const st* vbase = static_cast<const st*>(a.v) + static_cast<int64_t>(kvh) * a.v_sh;
-
-  auto load_tile = [&](int ts, KVTile<D>& T) {
-    const int64_t id0 = block_of(ts / bs);
-    const int bo0 = ts % bs;
-    int64_t id1 = id0;
-    int bo1 = bo0;
-    if (ts + 16 < kstop) {
-      id1 = block_of((ts + 16) / bs);
-      bo1 = (ts + 16) % bs;
-    }
-    const st* kp[2] = {kbase + id0 * a.k_sb + static_cast<int64_t>(bo0) * a.k_st,
-                       kbase + id1 * a.k_sb + static_cast<int64_t>(bo1) * a.k_st};
-    const st* vp[2] = {vbase + id0 * a.v_sb + static_cast<int64_t>(bo0) * a.v_st,
-                       vbase + id1 * a.v_sb + static_cast<int64_t>(bo1) * a.v_st};
-#pragma unroll
-    for (int sl = 0; sl < 2; ++sl)
-#pragma unroll
-      for (int c = 0; c < NC; ++c)
-        T.k[sl][c] = *reinterpret_cast<const u32x4*>(kp[sl] + k_lane + 32 * c);
-#pragma unroll
-    for (int s8 = 0; s8 < 8; ++s8) load_dwords<VW>(vp[s8 >> 2] + v_lane[s8 & 3], T.v[s8]);
-  };
-
+  u32x4 qf[NM][NC];  // Q as the B operand of S^T = K . Q^T
   float m[NM], l[NM];
-  f32x4 o[NM][EPL];
+  f32x4 o[NM][EPL];  // O^T: lane (n, g) holds head_dim EPL*(4g+j)+e of m-row n
+
+  // m-rows are the (query, head) pairs q0 + i / G, kvh * G + i % G of a row
+  // whose first query is global token qs; nq queries are valid.
+  __device__ void setup(const AttnArgs& a, int lane, int kvh, int64_t qs, int q0, int nq,
+                        int off) {
+    n = lane & 15;
+    g = lane >> 4;
+    const int G = a.G;
 #pragma unroll
-  for (int s = 0; s < NM; ++s) {
-    m[s] = -INFINITY;
-    l[s] = 0.f;
+    for (int s = 0; s < NM; ++s) {
+      const int i = 16 * s + n;
+      mq[s] = i / G;
+      mh[s] = kvh * G + (i % G);
+      mval[s] = mq[s] < nq && qs + q0 + mq[s] < a.total_q;
+      qpos[s] = mval[s] ? (a.causal ? off + q0 + mq[s] : INT_MAX) : -1;
 #pragma unroll
-    for (int e = 0; e < EPL; ++e) o[s][e] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int c = 0; c < NC; ++c) qf[s][c] = u32x4{0, 0, 0, 0};
+      if (mval[s]) {
+        const st* qp = static_cast<const st*>(a.q) + (qs + q0 + mq[s]) * a.q_st +
+                       static_cast<int64_t>(mh[s]) * a.q_sh;
+#pragma unroll
+        for (int c = 0; c < NC; ++c)
+          qf[s][c] = *reinterpret_cast<const u32x4*>(qp + 8 * (4 * c + g));
+      }
+      m[s] = -INFINITY;
+      l[s] = 0.f;
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) o[s][e] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
   }
 
-  auto compute_tile = [&](int ts, KVTile<D>& T) {
-    // S^T for the two 16-token slices.
-    f32x4 sc[2][NM];
+  // Online-softmax attention of every m-row over keys [kbeg, kstop) of `row`.
+  // kbeg is a multiple of 16.  qpos_min: smallest causal limit of the valid
+  // m-rows (keys up to it are visible to all of them).
+  // first_block >= 0: the physical block of key kbeg, known to the caller, so
+  // the first slice's loads need not wait for the block-table window.
+  __device__ void attend(const AttnArgs& a, int row, int kvh, int kbeg, int kstop,
+                         int qpos_min, int first_block = -1) {
+    const int lane = 16 * g + n;
+    const int bs = a.bs;
+    const int32_t* btrow = a.bt + static_cast<int64_t>(row) * a.bt_stride;
+    const int nb_row = min(static_cast<int64_t>((kstop + bs - 1) / bs), a.bt_stride);
+    // Block-table window: lane j holds the id of logical block win + j; a
+    // window of 64 blocks is loaded once before its tiles are walked.
+    int win = 0;
+    int bt_reg = 0;
+    const int first_lb = kbeg / bs;
+    auto block_of = [&](int lb) -> int64_t {
+      int64_t id = (first_block >= 0 && lb == first_lb) ? first_block
+                                                         : __builtin_amdgcn_readlane(bt_reg, lb - win);
+      id = id < 0 ? 0 : (id >= a.num_blocks ? a.num_blocks - 1 : id);
+      return id;
+    };
+    // Loop-invariant per-lane byte offsets inside a 16-token block slice.
+    const int k_lane = 2 * (n * static_cast<int>(a.k_st) + 8 * g);
+    int v_lane[4];
 #pragma unroll
-    for (int sl = 0; sl < 2; ++sl)
+    for (int j = 0; j < 4; ++j) v_lane[j] = 2 * ((4 * g + j) * static_cast<int>(a.v_st) + EPL * n);
+    const st* kbase = static_cast<const st*>(a.k) + static_cast<int64_t>(kvh) * a.k_sh;
+    const st* vbase = static_cast<const st*>(a.v) + static_cast<int64_t>(kvh) * a.v_sh;
+    // One descriptor per block: its kv head's rows, bounded by the block stride.
+    const int kbytes = static_cast<int>(2 * a.k_sb);
+    const int vbytes = static_cast<int>(2 * a.v_sb);
+
+    auto load_slice = [&](int ts, KVSlice<D>& T) {
+      const int64_t id = block_of(ts / bs);
+      const int bo = ts % bs;
+      const __amdgpu_buffer_rsrc_t kr = block_rsrc(kbase + id * a.k_sb, kbytes);
+      const __amdgpu_buffer_rsrc_t vr = block_rsrc(vbase + id * a.v_sb, vbytes);
+      const int ks = 2 * bo * static_cast<int>(a.k_st);
+      const int vs = 2 * bo * static_cast<int>(a.v_st);
+#pragma unroll
+      for (int c = 0; c < NC; ++c)
+        T.k[c] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(kr, k_lane + 64 * c, ks, 0));
+#pragma unroll
+      for (int j = 0; j < 4; ++j) buffer_dwords<VW>(vr, v_lane[j], vs, T.v[j]);
+    };
+
+    auto compute_slice = [&](int ts, KVSlice<D>& T) {
+      // S^T: lane (n, g) gets tokens ts + 4g + j of m-row n.
+      f32x4 sc[NM];
 #pragma unroll
       for (int s = 0; s < NM; ++s) {
         f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int c = 0; c < NC; ++c) acc = TT::mfma(T.k[sl][c], qf[s][c], acc);
-        sc[sl][s] = acc;
+        for (int c = 0; c < NC; ++c) acc = TT::mfma(T.k[c], qf[s][c], acc);
+        sc[s] = acc;
       }
-    const bool tail = ts + 32 > kstop;
-    const bool full = !tail && (ts + 31 <= qpos_min);
-#pragma unroll
-    for (int sl = 0; sl < 2; ++sl)
+      const bool tail = ts + 16 > kstop;
+      const bool full = !tail && (ts + 15 <= qpos_min);
 #pragma unroll
       for (int s = 0; s < NM; ++s)
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          float x = sc[sl][s][j] * a.scale_log2;
+          float x = sc[s][j] * a.scale_log2;
           if (!full) {
-            const int tk = ts + 16 * sl + 4 * g + j;
+            const int tk = ts + 4 * g + j;
             x = (tk < kstop && tk <= qpos[s]) ? x : -INFINITY;
           }
-          sc[sl][s][j] = x;
+          sc[s][j] = x;
         }
-    if (tail) {
-      // Keys past the end may hold any bit pattern; zero them so 0 * V stays 0.
+      if (tail) {
+        // Keys past the end may hold any bit pattern; zero them so 0 * V stays 0.
 #pragma unroll
-      for (int s8 = 0; s8 < 8; ++s8) {
-        const bool ok = ts + slot_token(g, s8) < kstop;
+        for (int j = 0; j < 4; ++j) {
+          const bool ok = ts + 4 * g + j < kstop;
 #pragma unroll
-        for (int w = 0; w < VW; ++w) T.v[s8][w] = ok ? T.v[s8][w] : 0u;
-      }
-    }
-    // Online softmax (base 2); P^T packed as the B operand of O^T += V^T . P^T.
-    u32x4 pb[NM];
-#pragma unroll
-    for (int s = 0; s < NM; ++s) {
-      float mx = fmaxf(fmaxf(fmaxf(sc[0][s][0], sc[0][s][1]), fmaxf(sc[0][s][2], sc[0][s][3])),
-                       fmaxf(fmaxf(sc[1][s][0], sc[1][s][1]), fmaxf(sc[1][s][2], sc[1][s][3])));
-      mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
-      mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
-      const float mnew = fmaxf(m[s], mx);
-      const float muse = (mnew == -INFINITY) ? 0.f : mnew;
-      const float corr = fast_exp2(m[s] - muse);
-      float pr[8];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        pr[j] = fast_exp2(sc[0][s][j] - muse);
-        pr[4 + j] = fast_exp2(sc[1][s][j] - muse);
-      }
-      float sum = ((pr[0] + pr[1]) + (pr[2] + pr[3])) + ((pr[4] + pr[5]) + (pr[6] + pr[7]));
-      l[s] = l[s] * corr + sum;
-      m[s] = mnew;
-      pb[s] = u32x4{TT::pack2(pr[0], pr[1]), TT::pack2(pr[2], pr[3]),
-                    TT::pack2(pr[4], pr[5]), TT::pack2(pr[6], pr[7])};
-#pragma unroll
-      for (int e = 0; e < EPL; ++e) o[s][e] *= corr;
-    }
-    // V^T A operand for head_dim values EPL*n + e, then O^T += V^T . P^T.
-#pragma unroll
-    for (int e = 0; e < EPL; ++e) {
-      const int w = e >> 1;
-      const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
-      const u32x4 vt = {__builtin_amdgcn_perm(T.v[1][w], T.v[0][w], sel),
-                        __builtin_amdgcn_perm(T.v[3][w], T.v[2][w], sel),
-                        __builtin_amdgcn_perm(T.v[5][w], T.v[4][w], sel),
-                        __builtin_amdgcn_perm(T.v[7][w], T.v[6][w], sel)};
-#pragma unroll
-      for (int s = 0; s < NM; ++s) o[s][e] = TT::mfma(vt, pb[s], o[s][e]);
-    }
-  };
-
-  // ---- key loop over windows of 64 blocks; with DB, tile i+1 is in flight
-  // while tile i computes ----
-  for (int wbeg = kbeg; wbeg < kstop; wbeg += 64 * bs) {
-    const int wend = min(kstop, wbeg + 64 * bs);
-    win = wbeg / bs;
-    bt_reg = (win + lane < nb_row) ? btrow[win + lane] : 0;
-    if constexpr (!DB) {
-      for (int ts = wbeg; ts < wend; ts += 32) {
-        KVTile<D> T;
-        load_tile(ts, T);
-        compute_tile(ts, T);
-      }
-    } else {
-      KVTile<D> A, B;
-      int ts = wbeg;
-      load_tile(ts, A);
-      while (true) {
-        bool more = ts + 32 < wend;
-        if (more) load_tile(ts + 32, B);
-        compute_tile(ts, A);
-        ts += 32;
-        if (!more) break;
-        more = ts + 32 < wend;
-        if (more) load_tile(ts + 32, A);
-        compute_tile(ts, B);
-        ts += 32;
-        if (!more) break;
-      }
-    }
-  }
-
-  // ---- finish: lane (n, g) holds O^T rows d = EPL*(4g+j)+e of m-row n ----
-  float ltot[NM];
-#pragma unroll
-  for (int s = 0; s < NM; ++s) {
-    float t = l[s] + __shfl_xor(l[s], 16, kWave);
-    ltot[s] = t + __shfl_xor(t, 32, kWave);
-  }
-
-  if (nparts == 1) {
-#pragma unroll
-    for (int s = 0; s < NM; ++s) {
-      if (!mval[s]) continue;
-      const int64_t t = static_cast<int64_t>(qs) + q0 + mq[s];
-      const float inv = ltot[s] > 0.f ? 1.f / ltot[s] : 0.f;
-      st* op = static_cast<st*>(a.o) + t * a.o_st + static_cast<int64_t>(mh[s]) * a.o_sh;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        uint32_t w[VW];
-#pragma unroll
-        for (int e2 = 0; e2 < VW; ++e2)
-          w[e2] = TT::pack2(o[s][2 * e2][j] * inv, o[s][2 * e2 + 1][j] * inv);
-        st* dp = op + EPL * (4 * g + j);
-        if constexpr (VW == 2) {
-          *reinterpret_cast<u32x2*>(dp) = u32x2{w[0], w[1]};
-        } else {
-#pragma unroll
-          for (int c = 0; c < VW / 4; ++c)
-            *reinterpret_cast<u32x4*>(dp + 8 * c) =
-                u32x4{w[4 * c], w[4 * c + 1], w[4 * c + 2], w[4 * c + 3]};
+          for (int w = 0; w < VW; ++w) T.v[j][w] = ok ? T.v[j][w] : 0u;
         }
       }
-      if (a.lse && g == 0)
-        a.lse[t * a.l_st + static_cast<int64_t>(mh[s]) * a.l_sh] =
-            ltot[s] > 0.f ? (m[s] + __log2f(ltot[s])) * kLn2 : -INFINITY;
+      // Online softmax (base 2); P^T packed as the B operand of O^T += V^T . P^T.
+      u32x2 pb[NM];
+#pragma unroll
+      for (int s = 0; s < NM; ++s) {
+        float mx = fmaxf(fmaxf(sc[s][0], sc[s][1]), fmaxf(sc[s][2], sc[s][3]));
+        mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
+        mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+        const float mnew = fmaxf(m[s], mx);
+        const float muse = (mnew == -INFINITY) ? 0.f : mnew;
+        const float corr = fast_exp2(m[s] - muse);
+        float pr[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) pr[j] = fast_exp2(sc[s][j] - muse);
+        l[s] = l[s] * corr + ((pr[0] + pr[1]) + (pr[2] + pr[3]));
+        m[s] = mnew;
+        pb[s] = u32x2{TT::pack2(pr[0], pr[1]), TT::pack2(pr[2], pr[3])};
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) o[s][e] *= corr;
+      }
+      // V^T A operand for head_dim values EPL*n + e, then O^T += V^T . P^T.
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) {
+        const int w = e >> 1;
+        const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
+        const u32x2 vt = {__builtin_amdgcn_perm(T.v[1][w], T.v[0][w], sel),
+                          __builtin_amdgcn_perm(T.v[3][w], T.v[2][w], sel)};
+#pragma unroll
+        for (int s = 0; s < NM; ++s) o[s][e] = TT::mfma16(vt, pb[s], o[s][e]);
+      }
+    };
+
+    // Windows of 64 blocks; with DB, slice i+1 is in flight while slice i computes.
+    for (int wbeg = kbeg; wbeg < kstop; wbeg += 64 * bs) {
+      const int wend = min(kstop, wbeg + 64 * bs);
+      win = wbeg / bs;
+      bt_reg = (win + lane < nb_row) ? btrow[win + lane] : 0;
+      if constexpr (!DB) {
+        for (int ts = wbeg; ts < wend; ts += 16) {
+          KVSlice<D> T;
+          load_slice(ts, T);
+          compute_slice(ts, T);
+        }
+      } else {
+        KVSlice<D> A, B;
+        int ts = wbeg;
+        load_slice(ts, A);
+        while (true) {
+          bool more = ts + 16 < wend;
+          if (more) load_slice(ts + 16, B);
+          compute_slice(ts, A);
+          ts += 16;
+          if (!more) break;
+          more = ts + 16 < wend;
+          if (more) load_slice(ts + 16, A);
+          compute_slice(ts, B);
+          ts += 16;
+          if (!more) break;
+        }
+      }
     }
-    return;
   }
 
-  // ---- split-K: store this partition for attn_merge_kernel ----
-  // Only the decode launch splits, so a row holds exactly one query.
+  // Row sums over the four lane groups that share an m-row.
+  __device__ void row_sums(float (&ltot)[NM]) const {
 #pragma unroll
-  for (int s = 0; s < NM; ++s) {
-    if (!mval[s]) continue;
-    const int64_t pidx = (static_cast<int64_t>(row) * a.Hq + mh[s]) * a.max_parts + p;
-    const float inv = ltot[s] > 0.f ? 1.f / ltot[s] : 0.f;
-    float* wp = a.ws_o + pidx * D;
+    for (int s = 0; s < NM; ++s) {
+      const float t = l[s] + __shfl_xor(l[s], 16, kWave);
+      ltot[s] = t + __shfl_xor(t, 32, kWave);
+    }
+  }
+
+  // Final O (q dtype) and natural-log LSE of m-row s, to token t.
+  __device__ void store_final(const AttnArgs& a, int s, int64_t t, float ltot) const {
+    const float inv = ltot > 0.f ? 1.f / ltot : 0.f;
+    st* op = static_cast<st*>(a.o) + t * a.o_st + static_cast<int64_t>(mh[s]) * a.o_sh;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      float* dp = wp + EPL * (4 * g + j);
+      uint32_t w[VW];
 #pragma unroll
-      for (int c = 0; c < EPL / 4; ++c)
-        *reinterpret_cast<f32x4*>(dp + 4 * c) =
-            f32x4{o[s][4 * c][j] * inv, o[s][4 * c + 1][j] * inv,
-                  o[s][4 * c + 2][j] * inv, o[s][4 * c + 3][j] * inv};
+      for (int e2 = 0; e2 < VW; ++e2)
+        w[e2] = TT::pack2(o[s][2 * e2][j] * inv, o[s][2 * e2 + 1][j] * inv);
+      st* dp = op + EPL * (4 * g + j);
+      if constexpr (VW == 2) {
+        *reinterpret_cast<u32x2*>(dp) = u32x2{w[0], w[1]};
+      } else {
+#pragma unroll
+        for (int c = 0; c < VW / 4; ++c)
+          *reinterpret_cast<u32x4*>(dp + 8 * c) =
+              u32x4{w[4 * c], w[4 * c + 1], w[4 * c + 2], w[4 * c + 3]};
+      }
     }
-    if (g == 0) a.ws_lse[pidx] = ltot[s] > 0.f ? m[s] + __log2f(ltot[s]) : -INFINITY;
+    if (a.lse && g == 0)
+      a.lse[t * a.l_st + static_cast<int64_t>(mh[s]) * a.l_sh] =
+          ltot > 0.f ? (m[s] + __log2f(ltot)) * kLn2 : -INFINITY;
+  }
+};
+
+// --------------------------------------------------------------- decode --
+// Decode time is set by the longest chain of dependent slice loads any wave
+// walks, and the tail appears as soon as waves run out of work at different
+// times.  So every wave gets a near-equal number of 16-token slices: a
+// (row, kv head) "segment" of n slices runs on ceil(n / T) waves of one
+// work-group, which merge their pieces through LDS.
+//  * With a host schedule (kvhot_paged_attention_schedule), T is chosen so
+//    that all waves fit on the device at once, segments are bin-packed into
+//    W-wave work-groups, and each wave reads its (row, kv head, slice range)
+//    descriptor.
+//  * Without one, work-group (group, partition, row) takes W/S kv heads of
+//    one row, S waves each (S from decode_splits), and work-groups without
+//    work exit.
+// A segment that is one of several key partitions of its row (rows longer
+// than the partition size) stores an (LSE, O) partial to HBM instead, and
+// attn_merge_kernel combines the partitions in a second launch.  (Merging
+// across work-groups inside one launch needs a device-scope release per wave,
+// which on gfx950 is an L2 write-back per wave -- far slower than a launch.)
+
+#ifndef KVHOT_SLICES_PER_WAVE
+#define KVHOT_SLICES_PER_WAVE 8
+#endif
+
+// Waves per kv head in grid mode for a partition of nslices slices: the
+// smallest power of two up to W that keeps each wave near
+// KVHOT_SLICES_PER_WAVE slices and leaves no more than Hkv kv heads to a
+// work-group (no idle waves).
+__host__ __device__ inline int decode_splits(int nslices, int W, int Hkv) {
+  int S = 1;
+  while (S < W && (S * KVHOT_SLICES_PER_WAVE < nslices || W / S > Hkv)) S *= 2;
+  return S;
+}
+
+// LDS of a decode work-group: per wave the normalised O of its G query heads,
+// their base-2 LSE and the wave's segment key (row, kv head, partition).
+__host__ __device__ constexpr int64_t decode_lds_floats(int64_t W, int64_t G, int64_t D) {
+  return W * G * D + W * G + 4 * W + 2 * W;
+}
+
+template <class TT, int D, int W>
+__global__ void __launch_bounds__(64 * W)
+attn_decode_kernel(const AttnArgs a) {
+  extern __shared__ float smem[];
+  using st = uint16_t;
+  // Wave-uniform values are pinned to SGPRs with readfirstlane: derived from
+  // threadIdx they would otherwise count as divergent, putting block ids and
+  // buffer descriptors in VGPRs (a waterfall loop around every load).
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int G = a.G;
+  const int PT = a.part_tokens;
+
+  // ---- this wave's segment piece: keys [16*s0, 16*s1) of (row, kvh) ----
+  int row = -1, kvh = 0, s0 = 0, s1 = 0;
+  int d_qs = 0, d_kend = 0, d_first = -1, d_off = 0;
+  if (a.sched) {
+    const int4* u = a.sched + 2 * (static_cast<int64_t>(blockIdx.x) * W + wave);
+    const int4 u0 = u[0], u1 = u[1];
+    row = u0.x;
+    kvh = u0.y;
+    s0 = u0.z;
+    s1 = u0.w;
+    d_qs = u1.x;
+    d_kend = u1.y;
+    d_first = u1.z;
+    d_off = u1.w;
+  } else {
+    const int r = blockIdx.z;
+    const int p = blockIdx.y;
+    if (a.q_lens[r] != 1) return;
+    const int kend = decode_visible_keys(a, r);
+    if (p >= max((kend + PT - 1) / PT, 1)) return;
+    const int kbeg = p * PT;
+    const int nsl = max((min(kend, kbeg + PT) - kbeg + 15) / 16, 0);
+    const int S = decode_splits(nsl, W, a.Hkv);
+    const int HW = W / S;
+    if (static_cast<int>(blockIdx.x) * HW >= a.Hkv) return;
+    const int h = blockIdx.x * HW + wave / S;
+    const int split = wave % S;
+    if (h < a.Hkv) {
+      row = r;
+      kvh = h;
+      s0 = kbeg / 16 + (nsl * split) / S;
+      s1 = kbeg / 16 + (nsl * (split + 1)) / S;
+    }
+  }
+  row = __builtin_amdgcn_readfirstlane(row);
+  kvh = __builtin_amdgcn_readfirstlane(kvh);
+  s0 = __builtin_amdgcn_readfirstlane(s0);
+  s1 = __builtin_amdgcn_readfirstlane(s1);
+  bool valid;
+  int kend, off;
+  int64_t qs;
+  if (a.sched) {  // the descriptor carries the row's metadata: no dependent loads
+    valid = row >= 0 && kvh >= 0 && kvh < a.Hkv;
+    kend = __builtin_amdgcn_readfirstlane(d_kend);
+    kend = static_cast<int>(min(static_cast<int64_t>(kend), static_cast<int64_t>(a.max_parts) * PT));
+    qs = __builtin_amdgcn_readfirstlane(d_qs);
+    off = __builtin_amdgcn_readfirstlane(d_off);
+    d_first = __builtin_amdgcn_readfirstlane(d_first);
+  } else {
+    valid = row >= 0 && kvh >= 0 && kvh < a.Hkv && a.q_lens[row] == 1;
+    kend = valid ? decode_visible_keys(a, row) : 0;
+    qs = valid ? a.q_starts[row] : 0;
+    off = valid ? a.q_offs[row] : 0;
+  }
+  valid = valid && qs >= 0 && qs < a.total_q;
+  const int kb = 16 * s0;
+  const int ke = min(kend, 16 * s1);
+
+  WaveAttn<TT, D, 1, false> wa;
+  wa.setup(a, lane, valid ? kvh : 0, qs, 0, valid ? 1 : 0, off);
+  if (valid && ke > kb) wa.attend(a, row, kvh, kb, ke, a.causal ? off : INT_MAX, d_first);
+  float ltot[1];
+  wa.row_sums(ltot);
+
+  float* so = smem;                                    // [W][G][D]
+  float* sl = smem + W * G * D;                        // [W][G]
+  int* sk = reinterpret_cast<int*>(sl + W * G);        // [W][4] (row, kvh, partition, parts)
+  int64_t* sq = reinterpret_cast<int64_t*>(sk + 4 * W); // [W] query token
+  if (wa.mval[0]) {
+    const float inv = ltot[0] > 0.f ? 1.f / ltot[0] : 0.f;
+    float* dst = so + (wave * G + wa.n) * D;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int e = 0; e < D / 16; e += 4)
+        *reinterpret_cast<f32x4*>(dst + (D / 16) * (4 * wa.g + j) + e) =
+            f32x4{wa.o[0][e][j] * inv, wa.o[0][e + 1][j] * inv, wa.o[0][e + 2][j] * inv,
+                  wa.o[0][e + 3][j] * inv};
+    if (wa.g == 0) sl[wave * G + wa.n] = ltot[0] > 0.f ? wa.m[0] + __log2f(ltot[0]) : -INFINITY;
+  }
+  if (lane == 0) {
+    sk[4 * wave + 0] = valid ? row : -1;
+    sk[4 * wave + 1] = kvh;
+    sk[4 * wave + 2] = kb / PT;
+    sk[4 * wave + 3] = valid ? max((kend + PT - 1) / PT, 1) : 0;
+    sq[wave] = qs;
+  }
+  __syncthreads();
+
+  // ---- merge every segment (maximal run of waves with one key) ----
+  auto same = [&](int x, int y) {
+    return sk[4 * x] == sk[4 * y] && sk[4 * x + 1] == sk[4 * y + 1] && sk[4 * x + 2] == sk[4 * y + 2];
+  };
+  for (int w0 = 0; w0 < W; ++w0) {
+    if (sk[4 * w0] < 0 || (w0 > 0 && same(w0 - 1, w0))) continue;
+    int w1 = w0 + 1;
+    while (w1 < W && same(w0, w1)) ++w1;
+    const int srow = sk[4 * w0], skvh = sk[4 * w0 + 1], sp = sk[4 * w0 + 2], snp = sk[4 * w0 + 3];
+    const int64_t sqs = sq[w0];
+    for (int it = threadIdx.x; it < G * (D / 4); it += 64 * W) {
+      const int hh = it / (D / 4);
+      const int d0 = 4 * (it % (D / 4));
+      float mx = -INFINITY;
+      for (int w = w0; w < w1; ++w) mx = fmaxf(mx, sl[w * G + hh]);
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+      float lsum = 0.f;
+      if (mx != -INFINITY) {
+        for (int w = w0; w < w1; ++w) {
+          const float wt = fast_exp2(sl[w * G + hh] - mx);
+          lsum += wt;
+          acc += wt * *reinterpret_cast<const f32x4*>(so + (w * G + hh) * D + d0);
+        }
+      }
+      const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
+      const int h = skvh * G + hh;
+      const float lse2 = lsum > 0.f ? mx + __log2f(lsum) : -INFINITY;
+      if (snp == 1) {
+        st* dp = static_cast<st*>(a.o) + sqs * a.o_st + static_cast<int64_t>(h) * a.o_sh + d0;
+        *reinterpret_cast<u32x2*>(dp) =
+            u32x2{TT::pack2(acc.x * inv, acc.y * inv), TT::pack2(acc.z * inv, acc.w * inv)};
+        if (a.lse && d0 == 0) a.lse[sqs * a.l_st + static_cast<int64_t>(h) * a.l_sh] = lse2 * kLn2;
+      } else {
+        const int64_t pidx = (static_cast<int64_t>(srow) * a.Hq + h) * a.max_parts + sp;
+        *reinterpret_cast<f32x4*>(a.ws_o + pidx * D + d0) = acc * inv;
+        if (d0 == 0) a.ws_lse[pidx] = lse2;
+      }
+    }
   }
 }
 
-// Combines the split-K partitions of decode rows: one lane per (row, query
-// head, 8 head_dim values).  Rows finished by a single partition are skipped;
-// the partition count is recomputed exactly as the split kernel did.
+// Combines the per-work-group partitions of decode rows: one lane per (row,
+// query head, 8 head_dim values).  Rows finished by a single partition are
+// skipped; the partition count is recomputed exactly as the decode kernel did.
 template <class TT, int D>
 __global__ void __launch_bounds__(256)
 attn_merge_kernel(const AttnArgs a) {
@@ -384,13 +547,8 @@ attn_merge_kernel(const AttnArgs a) {
   if (idx >= a.Hq * CH) return;
   const int h = idx / CH;
   const int c = idx % CH;
-  const int off = a.q_offs[row];
-  const int klen = a.k_lens[row];
-  int kend = a.causal ? min(klen, off + 1) : klen;
-  kend = max(kend, 0);
   const int PT = a.part_tokens;
-  kend = static_cast<int>(min(static_cast<int64_t>(kend), static_cast<int64_t>(a.max_parts) * PT));
-  const int nparts = (kend + PT - 1) / PT;
+  const int nparts = (decode_visible_keys(a, row) + PT - 1) / PT;
   if (nparts <= 1) return;
   const int64_t t = a.q_starts[row];
   if (t < 0 || t >= a.total_q) return;
@@ -398,26 +556,63 @@ attn_merge_kernel(const AttnArgs a) {
   const int64_t base = (static_cast<int64_t>(row) * a.Hq + h) * a.max_parts;
   float mmax = -INFINITY;
   for (int pp = 0; pp < nparts; ++pp) mmax = fmaxf(mmax, a.ws_lse[base + pp]);
-  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
   float lsum = 0.f;
   if (mmax != -INFINITY) {
     for (int pp = 0; pp < nparts; ++pp) {
       const float w = fast_exp2(a.ws_lse[base + pp] - mmax);
       lsum += w;
       const f32x4* src = reinterpret_cast<const f32x4*>(a.ws_o + (base + pp) * D + 8 * c);
-      const f32x4 x0 = src[0], x1 = src[1];
-      acc[0] += w * x0.x; acc[1] += w * x0.y; acc[2] += w * x0.z; acc[3] += w * x0.w;
-      acc[4] += w * x1.x; acc[5] += w * x1.y; acc[6] += w * x1.z; acc[7] += w * x1.w;
+      acc0 += w * src[0];
+      acc1 += w * src[1];
     }
   }
   const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
   st* dp = static_cast<st*>(a.o) + t * a.o_st + static_cast<int64_t>(h) * a.o_sh + 8 * c;
   *reinterpret_cast<u32x4*>(dp) =
-      u32x4{TT::pack2(acc[0] * inv, acc[1] * inv), TT::pack2(acc[2] * inv, acc[3] * inv),
-            TT::pack2(acc[4] * inv, acc[5] * inv), TT::pack2(acc[6] * inv, acc[7] * inv)};
+      u32x4{TT::pack2(acc0.x * inv, acc0.y * inv), TT::pack2(acc0.z * inv, acc0.w * inv),
+            TT::pack2(acc1.x * inv, acc1.y * inv), TT::pack2(acc1.z * inv, acc1.w * inv)};
   if (a.lse && c == 0)
     a.lse[t * a.l_st + static_cast<int64_t>(h) * a.l_sh] =
         lsum > 0.f ? (mmax + __log2f(lsum)) * kLn2 : -INFINITY;
+}
+
+// -------------------------------------------------------------- prefill --
+// One wave per (row, kv head, query block of 16*NM/G queries), no key split.
+template <class TT, int D, int NM>
+__global__ void __launch_bounds__(64)
+attn_prefill_kernel(const AttnArgs a) {
+  const int lane = threadIdx.x;
+  int row, kvh, qblk;
+  if (a.sched) {
+    const int4 u = a.sched[2 * static_cast<int64_t>(blockIdx.x)];
+    row = u.x;
+    kvh = u.y;
+    qblk = u.z;
+  } else {
+    row = blockIdx.z;
+    kvh = blockIdx.x % a.Hkv;
+    qblk = blockIdx.x / a.Hkv;
+  }
+  const int qlen = a.q_lens[row];
+  if (qlen < 2) return;
+  const int QPW = 16 * NM / a.G;
+  const int q0 = qblk * QPW;
+  if (q0 >= qlen) return;
+  const int nq = min(QPW, qlen - q0);
+  const int off = a.q_offs[row];
+  const int klen = a.k_lens[row];
+  const int kend = max(a.causal ? min(klen, off + q0 + nq) : klen, 0);
+  const int64_t qs = a.q_starts[row];
+
+  WaveAttn<TT, D, NM, false> wa;
+  wa.setup(a, lane, kvh, qs, q0, nq, off);
+  if (kend > 0) wa.attend(a, row, kvh, 0, kend, a.causal ? off + q0 : INT_MAX);
+  float ltot[NM];
+  wa.row_sums(ltot);
+#pragma unroll
+  for (int s = 0; s < NM; ++s)
+    if (wa.mval[s]) wa.store_final(a, s, qs + q0 + wa.mq[s], ltot[s]);
 }
 
 // ----------------------------------------------------------- VALU kernel --
@@ -510,11 +705,38 @@ attn_generic_kernel(const AttnArgs a) {
         l > 0.f ? (m + log2f(l)) * kLn2 : -INFINITY;
 }
 
+
 // ------------------------------------------------------------------ host --
+
+constexpr int64_t kMaxLdsBytes = 64 * 1024;
+#ifndef KVHOT_MIN_SLICES_PER_WAVE
+#define KVHOT_MIN_SLICES_PER_WAVE 8
+#endif
+#ifndef KVHOT_DECODE_ROUNDS
+#define KVHOT_DECODE_ROUNDS 1
+#endif
+#ifndef KVHOT_MAX_DECODE_WAVES
+#define KVHOT_MAX_DECODE_WAVES 16
+#endif
+// Lower bound on the planner's slices per wave: shorter chains cost more in
+// per-wave setup and merge than they save.
+constexpr int64_t kMinSlicesPerWave = KVHOT_MIN_SLICES_PER_WAVE;
+// Device-fulls of decode work-groups the planner aims for.
+constexpr int64_t kDecodeRounds = KVHOT_DECODE_ROUNDS;
+
+// Waves per decode work-group: 16 (head_dim <= 128, whose registers allow 4
+// waves per SIMD) when its LDS fits, else 8, else 0 (no MFMA path).
+static int decode_waves(int64_t G, int64_t D) {
+  if (KVHOT_MAX_DECODE_WAVES >= 16 && D <= 128 && decode_lds_floats(16, G, D) * 4 <= kMaxLdsBytes)
+    return 16;
+  if (decode_lds_floats(8, G, D) * 4 <= kMaxLdsBytes) return 8;
+  return 0;
+}
 
 struct Plan {
   bool mfma = false;
-  int part_tokens = 0;  // decode partition size (mfma path)
+  int waves = 0;        // waves per decode work-group
+  int part_tokens = 0;  // keys per decode partition
   int max_parts = 1;
   int64_t lse_bytes = 0, o_bytes = 0;
   int64_t workspace_bytes() const { return lse_bytes + o_bytes; }
@@ -527,31 +749,27 @@ static bool mfma_shape_ok(int64_t Hq, int64_t Hkv, int64_t D, int64_t bs, int dt
   if (D != 64 && D != 128 && D != 256) return false;
   if (bs % 16 != 0) return false;
   const int64_t G = Hq / Hkv;
-  return G == 1 || G == 2 || G == 4 || G == 8 || G == 16;
+  if (!(G == 1 || G == 2 || G == 4 || G == 8 || G == 16)) return false;
+  return decode_waves(G, D) > 0;
 }
 
-// Decode partition size: the largest of 512/256/128/64 keys that still gives
-// about 4096 (row, kv head, partition) waves over the batch.
-static int pick_partition(int64_t rows, int64_t Hkv, int64_t max_k) {
-  int pt = 512;
-  while (pt > 64 && rows * Hkv * ((max_k + pt - 1) / pt) < 4096) pt /= 2;
-  return pt;
-}
-
+// part_tokens = 0: grid-mode default of W * KVHOT_SLICES_PER_WAVE slices, so
+// no wave walks more than that many; a host schedule passes its own size.
 static Plan make_plan(int64_t rows, int64_t max_q, int64_t max_k, int64_t Hq,
                       int64_t Hkv, int64_t D, int64_t bs, int64_t part_tokens,
                       int dtype) {
   Plan pl;
   pl.mfma = mfma_shape_ok(Hq, Hkv, D, bs, dtype);
   if (!pl.mfma || max_q < 1 || max_k < 1) return pl;
+  pl.waves = decode_waves(Hq / Hkv, D);
   pl.part_tokens = part_tokens > 0 ? static_cast<int>(part_tokens)
-                                   : pick_partition(rows, Hkv, max_k);
-  pl.max_parts = static_cast<int>((max_k + pl.part_tokens - 1) / pl.part_tokens);
-  if (pl.max_parts > 65535) {
+                                   : 16 * pl.waves * KVHOT_SLICES_PER_WAVE;
+  const int64_t parts = (max_k + pl.part_tokens - 1) / pl.part_tokens;
+  if (parts > 65535) {
     pl.mfma = false;
-    pl.max_parts = 1;
     return pl;
   }
+  pl.max_parts = static_cast<int>(parts);
   if (pl.max_parts > 1) {
     pl.lse_bytes = round_up(rows * Hq * pl.max_parts * 4, 256);
     pl.o_bytes = rows * Hq * pl.max_parts * D * 4;
@@ -559,38 +777,210 @@ static Plan make_plan(int64_t rows, int64_t max_q, int64_t max_k, int64_t Hq,
   return pl;
 }
 
-#ifndef KVHOT_DECODE_DB
-#define KVHOT_DECODE_DB 1
-#endif
-constexpr bool kDecodeDB = KVHOT_DECODE_DB != 0;
+constexpr int prefill_nm(int64_t D) { return D <= 128 ? 4 : 2; }
 
-template <class TT, int D>
-static void launch_mfma(const AttnArgs& a, int64_t rows, int64_t max_q,
-                        int max_parts_dec, hipStream_t stream) {
-  // Decode rows: NM = 1, split-K.
-  {
-    AttnArgs d = a;
-    d.role = 0;
-    d.max_parts = max_parts_dec;
-    dim3 grid(static_cast<uint32_t>(a.Hkv), static_cast<uint32_t>(max_parts_dec),
-              static_cast<uint32_t>(rows));
-    hipLaunchKernelGGL((attn_mfma_kernel<TT, D, 1, kDecodeDB>), grid, dim3(64), 0, stream, d);
-    if (max_parts_dec > 1) {
-      dim3 mgrid(static_cast<uint32_t>((a.Hq * (D / 8) + 255) / 256),
-                 static_cast<uint32_t>(rows));
-      hipLaunchKernelGGL((attn_merge_kernel<TT, D>), mgrid, dim3(256), 0, stream, d);
+// Decode work-groups the current device holds at once, times their waves
+// (4096 when no device can be queried).
+template <class TT, int D, int W>
+static int decode_groups_per_cu(int64_t G) {
+  int n = 0;
+  const size_t lds = static_cast<size_t>(decode_lds_floats(W, G, D) * 4);
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, attn_decode_kernel<TT, D, W>, 64 * W, lds) !=
+      hipSuccess)
+    n = 0;
+  return n;
+}
+
+template <class TT>
+static int decode_groups_per_cu(int64_t D, int W, int64_t G) {
+  if (W == 16) {
+    if (D == 64) return decode_groups_per_cu<TT, 64, 16>(G);
+    if (D == 128) return decode_groups_per_cu<TT, 128, 16>(G);
+    return decode_groups_per_cu<TT, 256, 16>(G);
+  }
+  if (D == 64) return decode_groups_per_cu<TT, 64, 8>(G);
+  if (D == 128) return decode_groups_per_cu<TT, 128, 8>(G);
+  return decode_groups_per_cu<TT, 256, 8>(G);
+}
+
+static int64_t resident_decode_waves(int dtype, int64_t D, int W, int64_t G) {
+  int dev = 0, cus = 0;
+  int per = 0;
+  if (hipGetDevice(&dev) == hipSuccess &&
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess)
+    per = dtype == KVHOT_BF16 ? decode_groups_per_cu<BF16>(D, W, G)
+                              : decode_groups_per_cu<F16>(D, W, G);
+  if (cus <= 0 || per <= 0) {
+    (void)hipGetLastError();
+    return 4096;
+  }
+  return static_cast<int64_t>(cus) * per * W;
+}
+
+struct Segment {
+  int row, kvh, s0, s1, waves;
+};
+
+// Decode launch list: every (row, kv head, partition) segment of n slices
+// gets ceil(n / T) <= W waves, segments are packed best-fit-decreasing into
+// W-wave work-groups, and T is the smallest value >= kMinSlicesPerWave whose
+// packing fits on the device at once (so every wave walks <= T slices and
+// all of them run concurrently).  Returns the partition size used.
+static int64_t plan_decode(const int32_t* q_lens, const int32_t* k_lens, const int32_t* q_offs,
+                           const int32_t* q_starts, const int32_t* bt, int64_t bt_stride,
+                           int64_t bs, int64_t rows, int64_t Hkv, bool causal, int W,
+                           int64_t resident, int64_t given_pt, std::vector<int4>& out) {
+  std::vector<int64_t> kend(rows, -1);
+  int64_t total = 0;
+  for (int64_t r = 0; r < rows; ++r) {
+    if (q_lens[r] != 1) continue;
+    const int64_t klen = k_lens[r], off = q_offs[r];
+    kend[r] = std::max<int64_t>(causal ? std::min(klen, off + 1) : klen, 0);
+    total += std::max<int64_t>((kend[r] + 15) / 16, 1) * Hkv;
+  }
+  std::vector<Segment> segs;
+  std::vector<std::vector<int>> groups;  // segment indices per work-group
+  auto build = [&](int64_t T, int64_t PT) {
+    segs.clear();
+    groups.clear();
+    for (int64_t r = 0; r < rows; ++r) {
+      if (kend[r] < 0) continue;
+      const int64_t nparts = std::max<int64_t>((kend[r] + PT - 1) / PT, 1);
+      for (int64_t p = 0; p < nparts; ++p) {
+        const int64_t kb = p * PT, ke = std::min(kend[r], kb + PT);
+        const int64_t n = std::max<int64_t>((ke - kb + 15) / 16, 0);
+        const int w = static_cast<int>(std::min<int64_t>(std::max<int64_t>((n + T - 1) / T, 1), W));
+        for (int64_t h = 0; h < Hkv; ++h)
+          segs.push_back(Segment{static_cast<int>(r), static_cast<int>(h), static_cast<int>(kb / 16),
+                                 static_cast<int>(kb / 16 + n), w});
+      }
+    }
+    std::vector<int> order(segs.size());
+    for (size_t i = 0; i < order.size(); ++i) order[i] = static_cast<int>(i);
+    std::stable_sort(order.begin(), order.end(),
+                     [&](int x, int y) { return segs[x].waves > segs[y].waves; });
+    std::vector<std::vector<int>> by_free(W + 1);  // work-groups by free slots
+    std::vector<int> free_slots;
+    for (int si : order) {
+      const int w = segs[si].waves;
+      int f = w;
+      while (f <= W && by_free[f].empty()) ++f;
+      int gi;
+      if (f > W || f == W) {  // no partly used group fits: open a new one
+        gi = static_cast<int>(groups.size());
+        groups.emplace_back();
+        free_slots.push_back(W);
+        f = W;
+        if (!by_free[W].empty() && by_free[W].back() == gi) by_free[W].pop_back();
+      } else {
+        gi = by_free[f].back();
+        by_free[f].pop_back();
+      }
+      groups[gi].push_back(si);
+      free_slots[gi] = f - w;
+      if (free_slots[gi] > 0) by_free[free_slots[gi]].push_back(gi);
+    }
+  };
+  int64_t T, PT;
+  if (given_pt > 0) {
+    PT = given_pt;
+    T = std::max<int64_t>((PT / 16 + W - 1) / W, 1);
+    build(T, PT);
+  } else {
+    const int64_t target = std::max<int64_t>(resident, 1) * kDecodeRounds;
+    T = std::max<int64_t>(kMinSlicesPerWave, (total + target - 1) / target);
+    for (;;) {
+      PT = 16 * W * T;
+      build(T, PT);
+      if (static_cast<int64_t>(groups.size()) * W <= target || T >= (1 << 16)) break;
+      T += std::max<int64_t>(1, T / 8);
     }
   }
-  if (max_q >= 2) {
-    constexpr int NM = 4;
-    AttnArgs pf = a;
-    pf.role = 1;
-    pf.max_parts = 1;
-    pf.part_tokens = INT_MAX / 2;
+  // Two int4 per wave: (row, kv head, first slice, end slice) and (query
+  // token, visible keys, physical block of the first slice or -1, query
+  // position) -- everything a wave needs before its first K/V load.
+  out.clear();
+  for (const auto& g : groups) {
+    int used = 0;
+    for (int si : g) {
+      const Segment& sg = segs[si];
+      const int n = sg.s1 - sg.s0;
+      for (int i = 0; i < sg.waves; ++i) {
+        const int a0 = sg.s0 + (n * i) / sg.waves, a1 = sg.s0 + (n * (i + 1)) / sg.waves;
+        const int64_t lb = 16 * static_cast<int64_t>(a0) / bs;
+        const int first = lb < bt_stride ? bt[sg.row * bt_stride + lb] : -1;
+        out.push_back(int4{sg.row, sg.kvh, a0, a1});
+        out.push_back(int4{q_starts[sg.row], static_cast<int>(kend[sg.row]), first, q_offs[sg.row]});
+      }
+      used += sg.waves;
+    }
+    for (; used < W; ++used) {
+      out.push_back(int4{-1, 0, 0, 0});
+      out.push_back(int4{0, 0, -1, 0});
+    }
+  }
+  return PT;
+}
+
+// Prefill launch list: (row, kv head, query block) units, longest key range first.
+static void plan_prefill(const int32_t* q_lens, const int32_t* k_lens, const int32_t* q_offs,
+                         int64_t rows, int64_t Hkv, int64_t G, int64_t D, bool causal,
+                         std::vector<int4>& pre) {
+  for (int64_t r = 0; r < rows; ++r) {
+    const int64_t qlen = q_lens[r], klen = k_lens[r], off = q_offs[r];
+    if (qlen < 2) continue;
+    const int64_t qpw = 16 * prefill_nm(D) / G;
+    for (int64_t qb = 0; qb * qpw < qlen; ++qb) {
+      const int64_t q0 = qb * qpw, nq = std::min(qpw, qlen - q0);
+      const int64_t kend = std::max<int64_t>(causal ? std::min(klen, off + q0 + nq) : klen, 0);
+      for (int64_t h = 0; h < Hkv; ++h)
+        pre.push_back(int4{static_cast<int>(r), static_cast<int>(h), static_cast<int>(qb),
+                           static_cast<int>((kend + 15) / 16)});
+    }
+  }
+  std::stable_sort(pre.begin(), pre.end(), [](const int4& x, const int4& y) { return x.w > y.w; });
+  // Two int4 per work-group, like the decode descriptors (second one unused).
+  std::vector<int4> wide;
+  wide.reserve(2 * pre.size());
+  for (const int4& u : pre) {
+    wide.push_back(u);
+    wide.push_back(int4{0, 0, 0, 0});
+  }
+  pre.swap(wide);
+}
+
+template <class TT, int D, int W>
+static void launch_decode(const AttnArgs& a, int64_t rows, int64_t n_dec, hipStream_t stream) {
+  dim3 grid = a.sched ? dim3(static_cast<uint32_t>(n_dec / W))
+                      : dim3(static_cast<uint32_t>(a.Hkv), static_cast<uint32_t>(a.max_parts),
+                             static_cast<uint32_t>(rows));
+  const size_t lds = static_cast<size_t>(decode_lds_floats(W, a.G, D) * 4);
+  hipLaunchKernelGGL((attn_decode_kernel<TT, D, W>), grid, dim3(64 * W), lds, stream, a);
+}
+
+template <class TT, int D>
+static void launch_mfma(const AttnArgs& a, int waves, int64_t rows, int64_t max_q, int64_t n_dec,
+                        int64_t n_pre, hipStream_t stream) {
+  if (!a.sched || n_dec > 0) {
+    if (waves == 16)
+      launch_decode<TT, D, 16>(a, rows, n_dec, stream);
+    else
+      launch_decode<TT, D, 8>(a, rows, n_dec, stream);
+    if (a.max_parts > 1) {
+      dim3 mgrid(static_cast<uint32_t>((a.Hq * (D / 8) + 255) / 256),
+                 static_cast<uint32_t>(rows));
+      hipLaunchKernelGGL((attn_merge_kernel<TT, D>), mgrid, dim3(256), 0, stream, a);
+    }
+  }
+  if (a.sched ? n_pre > 0 : max_q >= 2) {
+    constexpr int NM = prefill_nm(D);
     const int64_t qpw = 16 * NM / a.G;
     const int64_t nqb = (max_q + qpw - 1) / qpw;
-    dim3 grid(static_cast<uint32_t>(a.Hkv * nqb), 1u, static_cast<uint32_t>(rows));
-    hipLaunchKernelGGL((attn_mfma_kernel<TT, D, NM, false>), grid, dim3(64), 0, stream, pf);
+    dim3 grid = a.sched ? dim3(static_cast<uint32_t>(n_pre))
+                        : dim3(static_cast<uint32_t>(a.Hkv * nqb), 1u, static_cast<uint32_t>(rows));
+    AttnArgs pa = a;
+    if (a.sched) pa.sched = a.sched + 2 * n_dec;
+    hipLaunchKernelGGL((attn_prefill_kernel<TT, D, NM>), grid, dim3(64), 0, stream, pa);
   }
 }
 
@@ -612,6 +1002,64 @@ extern "C" int64_t kvhot_paged_attention_workspace_bytes(
   return pl.workspace_bytes();
 }
 
+extern "C" int64_t kvhot_paged_attention_schedule(
+    const int32_t* q_lens, const int32_t* k_lens, const int32_t* q_starts,
+    const int32_t* q_pos_offsets, const int32_t* block_table, int64_t bt_row_stride,
+    int64_t num_rows, int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim,
+    int64_t block_size, int64_t partition_tokens, int is_causal, int dtype,
+    int32_t* units, int64_t capacity_units, int64_t* num_decode_units,
+    int64_t* num_prefill_units, int64_t* partition_tokens_used) {
+  clear_error();
+  if (num_rows < 0 || num_q_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0 ||
+      block_size <= 0 || partition_tokens < 0 || num_q_heads % num_kv_heads != 0 ||
+      dtype_size(dtype) == 0 || capacity_units < 0 || bt_row_stride < 0)
+    return set_error(KVHOT_EINVAL, "paged_attention_schedule: bad sizes");
+  if (num_rows > 0 && (!q_lens || !k_lens || !q_starts || !q_pos_offsets ||
+                       (bt_row_stride > 0 && !block_table)))
+    return set_error(KVHOT_EINVAL, "paged_attention_schedule: null host arrays");
+  if (partition_tokens != 0 && (partition_tokens % 32 != 0 || partition_tokens > (1 << 20)))
+    return set_error(KVHOT_EINVAL, "paged_attention_schedule: bad partition_tokens");
+  int64_t max_q = 0, max_k = 0;
+  for (int64_t r = 0; r < num_rows; ++r) {
+    if (q_lens[r] < 0 || k_lens[r] < 0)
+      return set_error(KVHOT_EINVAL, "paged_attention_schedule: negative length");
+    max_q = std::max<int64_t>(max_q, q_lens[r]);
+    max_k = std::max<int64_t>(max_k, k_lens[r]);
+  }
+  std::vector<int4> dec, pre;
+  const Plan pl = make_plan(num_rows, max_q, max_k, num_q_heads, num_kv_heads, head_dim,
+                            block_size, partition_tokens, dtype);
+  int64_t pt_used = partition_tokens;
+  if (pl.mfma) {
+    const int64_t G = num_q_heads / num_kv_heads;
+    const int64_t resident = resident_decode_waves(dtype, head_dim, pl.waves, G);
+    pt_used = plan_decode(q_lens, k_lens, q_pos_offsets, q_starts, block_table, bt_row_stride,
+                          block_size, num_rows, num_kv_heads, is_causal != 0, pl.waves, resident,
+                          partition_tokens, dec);
+    plan_prefill(q_lens, k_lens, q_pos_offsets, num_rows, num_kv_heads, G, head_dim,
+                 is_causal != 0, pre);
+    const Plan check = make_plan(num_rows, max_q, max_k, num_q_heads, num_kv_heads, head_dim,
+                                 block_size, pt_used, dtype);
+    if (!check.mfma) {  // too many partitions for the grid: no schedule
+      dec.clear();
+      pre.clear();
+      pt_used = partition_tokens;
+    }
+  }
+  if (partition_tokens_used) *partition_tokens_used = pt_used;
+  // Units are 8 int32 (two int4) each: decode waves, then prefill work-groups.
+  const int64_t n_dec = static_cast<int64_t>(dec.size() / 2);
+  const int64_t n_pre = static_cast<int64_t>(pre.size() / 2);
+  if (num_decode_units) *num_decode_units = n_dec;
+  if (num_prefill_units) *num_prefill_units = n_pre;
+  if (units && capacity_units >= n_dec + n_pre) {
+    int4* out = reinterpret_cast<int4*>(units);
+    std::copy(dec.begin(), dec.end(), out);
+    std::copy(pre.begin(), pre.end(), out + dec.size());
+  }
+  return n_dec + n_pre;
+}
+
 extern "C" int kvhot_paged_attention(
     const void* q, const int64_t q_strides[3], const void* k_cache,
     const int64_t k_cache_strides[4], const void* v_cache,
@@ -622,7 +1070,8 @@ extern "C" int kvhot_paged_attention(
     int64_t total_query, int64_t max_q_len, int64_t max_k_len,
     int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim,
     int64_t block_size, int64_t num_blocks, float scale, int is_causal,
-    int dtype, int64_t partition_tokens, void* workspace,
+    int dtype, int64_t partition_tokens, const int32_t* schedule,
+    int64_t num_decode_units, int64_t num_prefill_units, void* workspace,
     int64_t workspace_bytes, void* stream) {
   clear_error();
   const int64_t es = dtype_size(dtype);
@@ -647,9 +1096,9 @@ extern "C" int kvhot_paged_attention(
       num_q_heads > 65535)
     return set_error(KVHOT_EUNSUPPORTED, "paged_attention: rows, max_q_len or heads too large");
   if (partition_tokens != 0 &&
-      (partition_tokens % 32 != 0 || partition_tokens > 64 * block_size))
+      (partition_tokens % 32 != 0 || partition_tokens > (1 << 20)))
     return set_error(KVHOT_EINVAL,
-                     "paged_attention: partition_tokens must be a multiple of 32 and <= 64*block_size");
+                     "paged_attention: partition_tokens must be a multiple of 32 and <= 2^20");
 
   AttnArgs a{};
   a.q = q; a.q_st = q_strides[0]; a.q_sh = q_strides[1];
@@ -670,11 +1119,18 @@ extern "C" int kvhot_paged_attention(
   a.causal = is_causal ? 1 : 0;
   a.D = static_cast<int32_t>(head_dim);
   a.total_q = total_query;
+  const int64_t n_dec = schedule ? num_decode_units : 0;
+  const int64_t n_pre = schedule ? num_prefill_units : 0;
+  if (schedule && (n_dec < 0 || n_pre < 0 || n_dec > 0x7fffffff || n_pre > 0x7fffffff))
+    return set_error(KVHOT_EINVAL, "paged_attention: bad schedule unit counts");
+  a.sched = reinterpret_cast<const int4*>(schedule);
   a.max_parts = 1;
   hipStream_t s = static_cast<hipStream_t>(stream);
 
   Plan pl = make_plan(num_rows, max_q_len, max_k_len, num_q_heads, num_kv_heads, head_dim,
                       block_size, partition_tokens, dtype);
+  if (schedule && pl.mfma && n_dec % pl.waves != 0)
+    return set_error(KVHOT_EINVAL, "paged_attention: decode schedule is not whole work-groups");
   if (pl.mfma) {
     // 16-byte vector loads/stores need 16-byte aligned rows.
     const int64_t al = 16 / es;
@@ -697,7 +1153,8 @@ extern "C" int kvhot_paged_attention(
       a.ws_o = reinterpret_cast<float*>(ws + pl.lse_bytes);
     }
     a.part_tokens = pl.part_tokens;
-#define KVHOT_MFMA(TT, DD) launch_mfma<TT, DD>(a, num_rows, max_q_len, pl.max_parts, s)
+    a.max_parts = pl.max_parts;
+#define KVHOT_MFMA(TT, DD) launch_mfma<TT, DD>(a, pl.waves, num_rows, max_q_len, n_dec, n_pre, s)
     if (dtype == KVHOT_BF16) {
       if (head_dim == 64) KVHOT_MFMA(BF16, 64);
       else if (head_dim == 128) KVHOT_MFMA(BF16, 128);
@@ -713,7 +1170,6 @@ extern "C" int kvhot_paged_attention(
 
   if (head_dim > kGenericMaxD)
     return set_error(KVHOT_EUNSUPPORTED, "paged_attention: head_dim > 256");
-  a.role = 2;
   dim3 grid(static_cast<uint32_t>(num_q_heads), static_cast<uint32_t>(max_q_len),
             static_cast<uint32_t>(num_rows));
   if (dtype == KVHOT_F32)

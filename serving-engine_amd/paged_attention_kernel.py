@@ -14,14 +14,19 @@ reference:
 Differences a caller can see, all additive:
 
 * the metadata dict carries extra keys -- ``max_q_len``, ``max_k_len`` (host
-  ints, so no device->host sync per layer), and on a GPU device
-  ``slot_mapping`` / ``positions`` (int64, built on the device by
-  ``kvhot_build_slot_mapping``);
+  ints, so no device->host sync per layer), host copies ``host_q_lens``,
+  ``host_k_lens``, ``host_q_starts``, ``host_q_pos_offsets``,
+  ``host_block_table`` (from which the first attention call
+  of a step builds the work-group launch list that every layer then reuses),
+  and on a GPU device ``slot_mapping`` / ``positions`` (int64, built on the
+  device by ``kvhot_build_slot_mapping``);
 * the metadata arrays are views into one device buffer filled by a single
   host->device copy instead of five;
 * a query with no visible key yields o = 0 and l = -inf.
 """
 from __future__ import annotations
+
+import ctypes
 
 import numpy as np
 import torch
@@ -49,6 +54,44 @@ def _workspace(device: torch.device, stream: int, nbytes: int) -> torch.Tensor |
         ws = torch.empty(int(nbytes), dtype=torch.uint8, device=device)
         _WORKSPACES[key] = ws
     return ws
+
+
+def _schedule(metadata, device, hq, hkv, d, bs, pt, causal, dtype):
+    """(device units, n_decode, n_prefill, partition_tokens) of
+    kvhot_paged_attention_schedule for this step, built once per attention
+    shape from the host length copies and cached in the metadata dict;
+    (None, 0, 0, pt) without host copies."""
+    host_q = metadata.get("host_q_lens")
+    if host_q is None:
+        return None, 0, 0, pt
+    key = (hq, hkv, d, bs, pt, bool(causal), dtype, str(device))
+    cache = metadata.setdefault("_schedules", {})
+    hit = cache.get(key)
+    if hit is not None:
+        return hit
+    host_k = metadata["host_k_lens"]
+    host_off = metadata["host_q_pos_offsets"]
+    host_qs = metadata["host_q_starts"]
+    host_bt = metadata["host_block_table"]
+    lib = _lib.load()
+    n_dec, n_pre, pt_used = ctypes.c_int64(0), ctypes.c_int64(0), ctypes.c_int64(pt)
+    args = (host_q.ctypes.data, host_k.ctypes.data, host_qs.ctypes.data, host_off.ctypes.data,
+            host_bt.ctypes.data if host_bt.size else None, host_bt.shape[1] if host_bt.ndim == 2 else 0,
+            len(host_q), hq, hkv, d, bs, pt, 1 if causal else 0, dtype)
+    outs = (ctypes.byref(n_dec), ctypes.byref(n_pre), ctypes.byref(pt_used))
+    total = lib.kvhot_paged_attention_schedule(*args, None, 0, *outs)
+    if total < 0:
+        _lib.check(int(total), "kvhot_paged_attention_schedule")
+    if total == 0:
+        hit = (None, 0, 0, pt)
+    else:
+        units = torch.empty((total, 8), dtype=torch.int32, pin_memory=True)
+        got = lib.kvhot_paged_attention_schedule(*args, units.data_ptr(), total, *outs)
+        if got != total:
+            _lib.check(-1 if got >= 0 else int(got), "kvhot_paged_attention_schedule")
+        hit = (units.to(device, non_blocking=True), n_dec.value, n_pre.value, int(pt_used.value))
+    cache[key] = hit
+    return hit
 
 
 def _host_max(metadata: dict, key: str, src: str) -> int:
@@ -118,6 +161,8 @@ def paged_flash_attention(q, k_cache, v_cache, metadata, num_q_heads, num_kv_hea
 
     lib = _lib.load()
     stream = _lib.stream_handle(device)
+    sched, n_dec, n_pre, pt = _schedule(metadata, device, num_q_heads, num_kv_heads, head_dim,
+                                        block_size, pt, is_causal, dtype)
     need = lib.kvhot_paged_attention_workspace_bytes(
         num_rows, total_query, max_q, max_k, num_q_heads, num_kv_heads, head_dim,
         block_size, pt, dtype)
@@ -135,6 +180,7 @@ def paged_flash_attention(q, k_cache, v_cache, metadata, num_q_heads, num_kv_hea
         metadata["q_starts"].data_ptr(), metadata["q_pos_offsets"].data_ptr(),
         num_rows, total_query, max_q, max_k, num_q_heads, num_kv_heads, head_dim,
         block_size, num_blocks, float(scale), 1 if is_causal else 0, dtype, pt,
+        sched.data_ptr() if sched is not None else None, n_dec, n_pre,
         ws.data_ptr() if ws is not None else None, ws.numel() if ws is not None else 0,
         stream)
     _lib.check(status, "kvhot_paged_attention")
@@ -193,6 +239,11 @@ def build_paged_batch_metadata(scheduler_output, device="cuda"):
         "total_query": q_start,
         "max_q_len": int(per_row[0].max()) if r else 0,
         "max_k_len": int(per_row[1].max()) if r else 0,
+        "host_q_lens": np.ascontiguousarray(host[0:r]),
+        "host_k_lens": np.ascontiguousarray(host[r:2 * r]),
+        "host_q_starts": np.ascontiguousarray(host[2 * r:3 * r]),
+        "host_q_pos_offsets": np.ascontiguousarray(host[3 * r:4 * r]),
+        "host_block_table": bt_host,
     }
     if dev.type == "cuda":
         meta["slot_mapping"], meta["positions"] = build_slot_mapping(meta, block_size=BLOCK_SIZE)

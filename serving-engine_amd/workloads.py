@@ -278,4 +278,9 @@ def metadata_tensors(w: Workload, device="cuda") -> dict:
         "total_query": w.total_query,
         "max_q_len": w.max_q_len,
         "max_k_len": w.max_k_len,
+        "host_q_lens": q_lens,
+        "host_k_lens": k_lens,
+        "host_q_starts": q_starts,
+        "host_q_pos_offsets": offs,
+        "host_block_table": bt,
     }
