@@ -119,12 +119,13 @@ int kvhot_build_slot_mapping(const int32_t* block_table, int64_t bt_row_stride,
                              int64_t* positions, void* stream);
 
 /*
- * Workspace bytes kvhot_paged_attention needs for these sizes (0 if it needs
- * none): split-K partition results of decode rows, fully rewritten by each
- * call before they are read, so a workspace needs no initialisation and may
- * be reused by calls of any shape that fits.  Calls sharing a workspace must
- * be ordered on one stream.  Returns a negative KVHOT_E* code for invalid
- * sizes.
+ * Workspace bytes kvhot_paged_attention needs for these sizes when it is
+ * called WITHOUT a schedule (0 if it needs none): split-K partition results
+ * of decode rows, fully rewritten by each call before they are read, so a
+ * workspace needs no initialisation and may be reused by calls of any shape
+ * that fits.  Calls sharing a workspace must be ordered on one stream.
+ * Returns a negative KVHOT_E* code for invalid sizes.  (With a schedule, the
+ * size comes from kvhot_paged_attention_schedule.)
  */
 int64_t kvhot_paged_attention_workspace_bytes(
     int64_t num_rows, int64_t total_query, int64_t max_q_len,
@@ -135,20 +136,24 @@ int64_t kvhot_paged_attention_workspace_bytes(
  * Launch list ("schedule") for kvhot_paged_attention, built on the host from
  * HOST copies of q_lens, k_lens, q_starts, q_pos_offsets and the block table,
  * with the head counts, head_dim, block_size, is_causal and dtype the
- * attention call will get.  Decode rows are cut into pieces of near-equal
- * length, sized so that all decode waves fit on the current device at once,
- * and packed into work-groups: num_decode_units per-wave descriptors (whole
- * work-groups; each carries its row's metadata and first block so the wave's
- * first K/V loads depend on nothing else), followed by num_prefill_units
- * per-work-group prefill units, 8 int32 per unit, longest first.  partition_tokens = 0 lets the planner choose the key
- * partition; the size it used is returned in *partition_tokens_used and must
- * be passed as partition_tokens to kvhot_paged_attention (and to the
- * workspace query).  Returns the total unit count (units are written when
- * `units` is non-NULL and capacity_units suffices) or a negative KVHOT_E*
- * code.  A schedule depends only on the step's lengths, so one upload serves
- * every layer of an engine step.  Without a schedule the attention launch
- * covers the padded grid of (row, partition, head group), and work-groups
- * without work still cost a launch slot each.
+ * attention call will get.  The (row, kv head) key ranges of decode rows are
+ * laid end to end and cut into equal numbers of 16-token slices per decode
+ * work-group, one device-full of work-groups; a range cut in two becomes
+ * "parts" in different work-groups.  Units of 8 int32, in order:
+ * num_decode_units per-wave descriptors (whole work-groups; each carries its
+ * row's metadata and first block, so the wave's first K/V loads depend on
+ * nothing else), num_prefill_units per-work-group prefill units (longest
+ * first), num_merge_units units, one per decode range cut into parts.
+ * partition_tokens > 0 (a multiple of 32 up to 2^20) first cuts every decode
+ * row into partitions of that many keys, which are then never cut further;
+ * 0 leaves the cuts to the planner.  *workspace_bytes receives the workspace
+ * the attention call needs with this schedule (0: none).  Returns the total
+ * unit count (units are written when `units` is non-NULL and capacity_units
+ * suffices) or a negative KVHOT_E* code.  A schedule depends only on the
+ * step's lengths, so one upload serves every layer of an engine step.
+ * Without a schedule the attention launch covers the padded grid of (row,
+ * partition, head group), and work-groups without work still cost a launch
+ * slot each.
  */
 int64_t kvhot_paged_attention_schedule(
     const int32_t* q_lens, const int32_t* k_lens, const int32_t* q_starts,
@@ -157,7 +162,7 @@ int64_t kvhot_paged_attention_schedule(
     int64_t head_dim, int64_t block_size, int64_t partition_tokens,
     int is_causal, int dtype, int32_t* units, int64_t capacity_units,
     int64_t* num_decode_units, int64_t* num_prefill_units,
-    int64_t* partition_tokens_used);
+    int64_t* num_merge_units, int64_t* workspace_bytes);
 
 /*
  * Paged attention forward over a ragged batch of rows (prefill chunks and
@@ -169,16 +174,20 @@ int64_t kvhot_paged_attention_schedule(
  *   out[t, h, :] = softmax_j(scale * q[t,h,:] . k_j) @ v_j   (fp32 accumulate)
  *   lse[t, h]    = natural-log logsumexp_j(scale * q[t,h,:] . k_j)
  * A query with no visible key gets out = 0 and lse = -inf.
- * Rows with n_q == 1 run the split-K flash-decoding kernel (partitions of
- * partition_tokens keys, then a merge launch when any row has more than one
- * partition); rows with n_q >= 2 run the chunked-prefill kernel.  max_q_len / max_k_len must bound
+ * Rows with n_q == 1 run the split-K flash-decoding kernel, plus a merge
+ * launch when a decode row was split across work-groups; rows with
+ * n_q >= 2 run the chunked-prefill kernel.  max_q_len / max_k_len must bound
  * q_lens / k_lens (they size the grid; no device->host sync is made).
- * partition_tokens (keys per decode work-group) = 0 picks a size; otherwise a
- * multiple of 32 up to 2^20.  schedule: device copy of the units from
- * kvhot_paged_attention_schedule for exactly these lengths and sizes, or NULL.
- * lse may be NULL.  out has the dtype of q, k_cache and v_cache; lse is fp32.
- * Replaces paged_flash_attention + paged_flash_fwd_kernel
- * (serving_engine/paged_attention_kernel.py:16-160).
+ * schedule: device copy of the units from kvhot_paged_attention_schedule for
+ * exactly these lengths and sizes, with its three unit counts and a workspace
+ * of the size it reported; or NULL, and then partition_tokens (keys per
+ * decode partition; 0 picks a size, otherwise a multiple of 32 up to 2^20)
+ * and kvhot_paged_attention_workspace_bytes apply.  With a schedule, decode
+ * waves of one work-group share out their slices at run time, so the
+ * summation order, and with it the last bits of out and lse, can differ from
+ * call to call.  lse may be NULL.  out has the dtype of q, k_cache and
+ * v_cache; lse is fp32.  Replaces paged_flash_attention +
+ * paged_flash_fwd_kernel (serving_engine/paged_attention_kernel.py:16-160).
  */
 int kvhot_paged_attention(
     const void* q, const int64_t q_strides[3],
@@ -193,8 +202,9 @@ int kvhot_paged_attention(
     int64_t num_kv_heads, int64_t head_dim, int64_t block_size,
     int64_t num_blocks, float scale, int is_causal, int dtype,
     int64_t partition_tokens, const int32_t* schedule,
-    int64_t num_decode_units, int64_t num_prefill_units, void* workspace,
-    int64_t workspace_bytes, void* stream);
+    int64_t num_decode_units, int64_t num_prefill_units,
+    int64_t num_merge_units, void* workspace, int64_t workspace_bytes,
+    void* stream);
 
 #ifdef __cplusplus
 }

@@ -54,8 +54,11 @@ struct AttnArgs {
   const int32_t* k_lens;
   const int32_t* q_starts;
   const int32_t* q_offs;
-  float* ws_lse;  // [rows, Hq, max_parts] log2-domain partition LSE
-  float* ws_o;    // [rows, Hq, max_parts, D] normalised partition output
+  // Split-K partials, P = num_partials of them: ws_o [P][G][D] normalised
+  // output, ws_lse [P][G] log2-domain LSE of a (row, kv head, part) piece.
+  float* ws_lse;
+  float* ws_o;
+  int64_t num_partials;
   int64_t num_blocks;
   int32_t Hq, Hkv, G, bs;
   int32_t part_tokens, max_parts;
@@ -67,6 +70,8 @@ struct AttnArgs {
   // prefill: two int4 per work-group), or null: then the grid enumerates every
   // (row, partition, head group) and work-groups without work exit.
   const int4* sched;
+  const int4* merge_units;  // schedule: two int4 per split decode segment
+  int32_t dec_slots;  // LDS (LSE, O) slots of a decode work-group, >= its waves
 };
 
 __device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
@@ -175,140 +180,129 @@ struct WaveAttn {
     }
   }
 
-  // Online-softmax attention of every m-row over keys [kbeg, kstop) of `row`.
-  // kbeg is a multiple of 16.  qpos_min: smallest causal limit of the valid
-  // m-rows (keys up to it are visible to all of them).
-  // first_block >= 0: the physical block of key kbeg, known to the caller, so
-  // the first slice's loads need not wait for the block-table window.
-  __device__ void attend(const AttnArgs& a, int row, int kvh, int kbeg, int kstop,
-                         int qpos_min, int first_block = -1) {
+  // Issues the loads of one 16-token slice of kv head kvh: tokens bo..bo+15
+  // of physical block id.
+  __device__ void load_slice(const AttnArgs& a, int kvh, int64_t id, int bo, KVSlice<D>& T) const {
+    // Per-lane byte offsets inside the slice; one descriptor per block, over
+    // this kv head's rows and bounded by the block stride.
+    const int k_lane = 2 * (n * static_cast<int>(a.k_st) + 8 * g);
+    const st* kb = static_cast<const st*>(a.k) + static_cast<int64_t>(kvh) * a.k_sh + id * a.k_sb;
+    const st* vb = static_cast<const st*>(a.v) + static_cast<int64_t>(kvh) * a.v_sh + id * a.v_sb;
+    const __amdgpu_buffer_rsrc_t kr = block_rsrc(kb, static_cast<int>(2 * a.k_sb));
+    const __amdgpu_buffer_rsrc_t vr = block_rsrc(vb, static_cast<int>(2 * a.v_sb));
+    const int ks = 2 * bo * static_cast<int>(a.k_st);
+    const int vs = 2 * bo * static_cast<int>(a.v_st);
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+      T.k[c] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(kr, k_lane + 64 * c, ks, 0));
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      buffer_dwords<VW>(vr, 2 * ((4 * g + j) * static_cast<int>(a.v_st) + EPL * n), vs, T.v[j]);
+  }
+
+  // Folds the slice of keys ts..ts+15 into the online softmax.  Keys at or
+  // past kstop, and keys past an m-row's causal limit, are masked; qpos_min is
+  // the smallest causal limit of the valid m-rows (keys up to it are visible
+  // to all of them).
+  __device__ void compute_slice(const AttnArgs& a, int ts, int kstop, int qpos_min, KVSlice<D>& T) {
+    // S^T: lane (n, g) gets tokens ts + 4g + j of m-row n.
+    f32x4 sc[NM];
+#pragma unroll
+    for (int s = 0; s < NM; ++s) {
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int c = 0; c < NC; ++c) acc = TT::mfma(T.k[c], qf[s][c], acc);
+      sc[s] = acc;
+    }
+    const bool tail = ts + 16 > kstop;
+    const bool full = !tail && (ts + 15 <= qpos_min);
+#pragma unroll
+    for (int s = 0; s < NM; ++s)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        float x = sc[s][j] * a.scale_log2;
+        if (!full) {
+          const int tk = ts + 4 * g + j;
+          x = (tk < kstop && tk <= qpos[s]) ? x : -INFINITY;
+        }
+        sc[s][j] = x;
+      }
+    if (tail) {
+      // Keys past the end may hold any bit pattern; zero them so 0 * V stays 0.
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const bool ok = ts + 4 * g + j < kstop;
+#pragma unroll
+        for (int w = 0; w < VW; ++w) T.v[j][w] = ok ? T.v[j][w] : 0u;
+      }
+    }
+    // Online softmax (base 2); P^T packed as the B operand of O^T += V^T . P^T.
+    u32x2 pb[NM];
+#pragma unroll
+    for (int s = 0; s < NM; ++s) {
+      float mx = fmaxf(fmaxf(sc[s][0], sc[s][1]), fmaxf(sc[s][2], sc[s][3]));
+      mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
+      mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+      const float mnew = fmaxf(m[s], mx);
+      const float muse = (mnew == -INFINITY) ? 0.f : mnew;
+      const float corr = fast_exp2(m[s] - muse);
+      float pr[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) pr[j] = fast_exp2(sc[s][j] - muse);
+      l[s] = l[s] * corr + ((pr[0] + pr[1]) + (pr[2] + pr[3]));
+      m[s] = mnew;
+      pb[s] = u32x2{TT::pack2(pr[0], pr[1]), TT::pack2(pr[2], pr[3])};
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) o[s][e] *= corr;
+    }
+    // V^T A operand for head_dim values EPL*n + e, then O^T += V^T . P^T.
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) {
+      const int w = e >> 1;
+      const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
+      const u32x2 vt = {__builtin_amdgcn_perm(T.v[1][w], T.v[0][w], sel),
+                        __builtin_amdgcn_perm(T.v[3][w], T.v[2][w], sel)};
+#pragma unroll
+      for (int s = 0; s < NM; ++s) o[s][e] = TT::mfma16(vt, pb[s], o[s][e]);
+    }
+  }
+
+  // Online-softmax attention of every m-row over keys [kbeg, kstop) of `row`
+  // (kbeg a multiple of 16), walked in order.
+  __device__ void attend(const AttnArgs& a, int row, int kvh, int kbeg, int kstop, int qpos_min) {
     const int lane = 16 * g + n;
     const int bs = a.bs;
     const int32_t* btrow = a.bt + static_cast<int64_t>(row) * a.bt_stride;
     const int nb_row = min(static_cast<int64_t>((kstop + bs - 1) / bs), a.bt_stride);
-    // Block-table window: lane j holds the id of logical block win + j; a
-    // window of 64 blocks is loaded once before its tiles are walked.
-    int win = 0;
-    int bt_reg = 0;
-    const int first_lb = kbeg / bs;
-    auto block_of = [&](int lb) -> int64_t {
-      int64_t id = (first_block >= 0 && lb == first_lb) ? first_block
-                                                         : __builtin_amdgcn_readlane(bt_reg, lb - win);
-      id = id < 0 ? 0 : (id >= a.num_blocks ? a.num_blocks - 1 : id);
-      return id;
-    };
-    // Loop-invariant per-lane byte offsets inside a 16-token block slice.
-    const int k_lane = 2 * (n * static_cast<int>(a.k_st) + 8 * g);
-    int v_lane[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) v_lane[j] = 2 * ((4 * g + j) * static_cast<int>(a.v_st) + EPL * n);
-    const st* kbase = static_cast<const st*>(a.k) + static_cast<int64_t>(kvh) * a.k_sh;
-    const st* vbase = static_cast<const st*>(a.v) + static_cast<int64_t>(kvh) * a.v_sh;
-    // One descriptor per block: its kv head's rows, bounded by the block stride.
-    const int kbytes = static_cast<int>(2 * a.k_sb);
-    const int vbytes = static_cast<int>(2 * a.v_sb);
-
-    auto load_slice = [&](int ts, KVSlice<D>& T) {
-      const int64_t id = block_of(ts / bs);
-      const int bo = ts % bs;
-      const __amdgpu_buffer_rsrc_t kr = block_rsrc(kbase + id * a.k_sb, kbytes);
-      const __amdgpu_buffer_rsrc_t vr = block_rsrc(vbase + id * a.v_sb, vbytes);
-      const int ks = 2 * bo * static_cast<int>(a.k_st);
-      const int vs = 2 * bo * static_cast<int>(a.v_st);
-#pragma unroll
-      for (int c = 0; c < NC; ++c)
-        T.k[c] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(kr, k_lane + 64 * c, ks, 0));
-#pragma unroll
-      for (int j = 0; j < 4; ++j) buffer_dwords<VW>(vr, v_lane[j], vs, T.v[j]);
-    };
-
-    auto compute_slice = [&](int ts, KVSlice<D>& T) {
-      // S^T: lane (n, g) gets tokens ts + 4g + j of m-row n.
-      f32x4 sc[NM];
-#pragma unroll
-      for (int s = 0; s < NM; ++s) {
-        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int c = 0; c < NC; ++c) acc = TT::mfma(T.k[c], qf[s][c], acc);
-        sc[s] = acc;
-      }
-      const bool tail = ts + 16 > kstop;
-      const bool full = !tail && (ts + 15 <= qpos_min);
-#pragma unroll
-      for (int s = 0; s < NM; ++s)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          float x = sc[s][j] * a.scale_log2;
-          if (!full) {
-            const int tk = ts + 4 * g + j;
-            x = (tk < kstop && tk <= qpos[s]) ? x : -INFINITY;
-          }
-          sc[s][j] = x;
-        }
-      if (tail) {
-        // Keys past the end may hold any bit pattern; zero them so 0 * V stays 0.
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const bool ok = ts + 4 * g + j < kstop;
-#pragma unroll
-          for (int w = 0; w < VW; ++w) T.v[j][w] = ok ? T.v[j][w] : 0u;
-        }
-      }
-      // Online softmax (base 2); P^T packed as the B operand of O^T += V^T . P^T.
-      u32x2 pb[NM];
-#pragma unroll
-      for (int s = 0; s < NM; ++s) {
-        float mx = fmaxf(fmaxf(sc[s][0], sc[s][1]), fmaxf(sc[s][2], sc[s][3]));
-        mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
-        mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
-        const float mnew = fmaxf(m[s], mx);
-        const float muse = (mnew == -INFINITY) ? 0.f : mnew;
-        const float corr = fast_exp2(m[s] - muse);
-        float pr[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) pr[j] = fast_exp2(sc[s][j] - muse);
-        l[s] = l[s] * corr + ((pr[0] + pr[1]) + (pr[2] + pr[3]));
-        m[s] = mnew;
-        pb[s] = u32x2{TT::pack2(pr[0], pr[1]), TT::pack2(pr[2], pr[3])};
-#pragma unroll
-        for (int e = 0; e < EPL; ++e) o[s][e] *= corr;
-      }
-      // V^T A operand for head_dim values EPL*n + e, then O^T += V^T . P^T.
-#pragma unroll
-      for (int e = 0; e < EPL; ++e) {
-        const int w = e >> 1;
-        const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
-        const u32x2 vt = {__builtin_amdgcn_perm(T.v[1][w], T.v[0][w], sel),
-                          __builtin_amdgcn_perm(T.v[3][w], T.v[2][w], sel)};
-#pragma unroll
-        for (int s = 0; s < NM; ++s) o[s][e] = TT::mfma16(vt, pb[s], o[s][e]);
-      }
-    };
-
-    // Windows of 64 blocks; with DB, slice i+1 is in flight while slice i computes.
+    // Windows of 64 blocks: lane j holds the id of logical block win + j,
+    // loaded once before the window's slices are walked.
     for (int wbeg = kbeg; wbeg < kstop; wbeg += 64 * bs) {
       const int wend = min(kstop, wbeg + 64 * bs);
-      win = wbeg / bs;
-      bt_reg = (win + lane < nb_row) ? btrow[win + lane] : 0;
+      const int win = wbeg / bs;
+      const int bt_reg = (win + lane < nb_row) ? btrow[win + lane] : 0;
+      auto block_of = [&](int ts) -> int64_t {
+        int64_t id = __builtin_amdgcn_readlane(bt_reg, ts / bs - win);
+        return id < 0 ? 0 : (id >= a.num_blocks ? a.num_blocks - 1 : id);
+      };
       if constexpr (!DB) {
         for (int ts = wbeg; ts < wend; ts += 16) {
           KVSlice<D> T;
-          load_slice(ts, T);
-          compute_slice(ts, T);
+          load_slice(a, kvh, block_of(ts), ts % bs, T);
+          compute_slice(a, ts, kstop, qpos_min, T);
         }
       } else {
         KVSlice<D> A, B;
         int ts = wbeg;
-        load_slice(ts, A);
+        load_slice(a, kvh, block_of(ts), ts % bs, A);
         while (true) {
           bool more = ts + 16 < wend;
-          if (more) load_slice(ts + 16, B);
-          compute_slice(ts, A);
+          if (more) load_slice(a, kvh, block_of(ts + 16), (ts + 16) % bs, B);
+          compute_slice(a, ts, kstop, qpos_min, A);
           ts += 16;
           if (!more) break;
           more = ts + 16 < wend;
-          if (more) load_slice(ts + 16, A);
-          compute_slice(ts, B);
+          if (more) load_slice(a, kvh, block_of(ts + 16), (ts + 16) % bs, A);
+          compute_slice(a, ts, kstop, qpos_min, B);
           ts += 16;
           if (!more) break;
         }
@@ -352,23 +346,27 @@ struct WaveAttn {
 };
 
 // --------------------------------------------------------------- decode --
-// Decode time is set by the longest chain of dependent slice loads any wave
-// walks, and the tail appears as soon as waves run out of work at different
-// times.  So every wave gets a near-equal number of 16-token slices: a
-// (row, kv head) "segment" of n slices runs on ceil(n / T) waves of one
-// work-group, which merge their pieces through LDS.
-//  * With a host schedule (kvhot_paged_attention_schedule), T is chosen so
-//    that all waves fit on the device at once, segments are bin-packed into
-//    W-wave work-groups, and each wave reads its (row, kv head, slice range)
-//    descriptor.
-//  * Without one, work-group (group, partition, row) takes W/S kv heads of
-//    one row, S waves each (S from decode_splits), and work-groups without
-//    work exit.
-// A segment that is one of several key partitions of its row (rows longer
-// than the partition size) stores an (LSE, O) partial to HBM instead, and
-// attn_merge_kernel combines the partitions in a second launch.  (Merging
-// across work-groups inside one launch needs a device-scope release per wave,
-// which on gfx950 is an L2 write-back per wave -- far slower than a launch.)
+// A decode row's keys are cut into (row, kv head, partition) segments, and a
+// segment into "ranges" of 16-token slices, one range per wave of a
+// work-group (host schedule from kvhot_paged_attention_schedule, or the grid:
+// work-group (group, partition, row) takes W/S kv heads of one row, S waves
+// each, S from decode_splits).
+//
+// Waves of one CU stream at very different rates (measured: equal ranges end
+// up to 20 us apart inside one work-group, while work-group means agree to a
+// few percent), so ranges are only a starting point.  Each wave claims its
+// slices one at a time from an LDS counter; when its range is used up it
+// claims slices from the range with the most left, first among waves of its
+// own segment (the online softmax takes keys in any order), then from other
+// segments.  Every (wave, segment) pair a wave worked on leaves a normalised
+// (LSE, O) in an LDS slot: its own slot first, then slots from a pool of
+// `dec_slots - W` (when the pool is empty the wave stops taking new segments).
+// After a barrier the first wave of each segment merges that segment's slots.
+// A segment that is one of several partitions of its row stores an (LSE, O)
+// partial to HBM instead, and attn_merge_kernel combines the partitions in a
+// second launch.  (Merging across work-groups inside one launch needs a
+// device-scope release per wave, which on gfx950 is an L2 write-back per wave
+// -- far slower than a launch.)
 
 #ifndef KVHOT_SLICES_PER_WAVE
 #define KVHOT_SLICES_PER_WAVE 8
@@ -384,10 +382,19 @@ __host__ __device__ inline int decode_splits(int nslices, int W, int Hkv) {
   return S;
 }
 
-// LDS of a decode work-group: per wave the normalised O of its G query heads,
-// their base-2 LSE and the wave's segment key (row, kv head, partition).
-__host__ __device__ constexpr int64_t decode_lds_floats(int64_t W, int64_t G, int64_t D) {
-  return W * G * D + W * G + 4 * W + 2 * W;
+// LDS of a decode work-group with S slots, in 4-byte words: per slot the
+// normalised O [G][D] and base-2 LSE [G] of its query heads and its segment
+// key (row, kv head, part); per wave the claim counter, range end and segment
+// description [8]; the slot-pool counter.
+constexpr int kDecInfo = 8;
+__host__ __device__ constexpr int64_t decode_lds_words(int64_t W, int64_t S, int64_t G, int64_t D) {
+  return S * G * D + S * G + 4 * S + (2 + kDecInfo) * W + 1;
+}
+
+__device__ inline int wave_max_int(int x) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) x = max(x, __shfl_xor(x, o, kWave));
+  return x;
 }
 
 template <class TT, int D, int W>
@@ -402,179 +409,337 @@ attn_decode_kernel(const AttnArgs a) {
   const int lane = threadIdx.x & 63;
   const int G = a.G;
   const int PT = a.part_tokens;
+  const int S = a.dec_slots;
 
-  // ---- this wave's segment piece: keys [16*s0, 16*s1) of (row, kvh) ----
-  int row = -1, kvh = 0, s0 = 0, s1 = 0;
-  int d_qs = 0, d_kend = 0, d_first = -1, d_off = 0;
+  // ---- this wave's range: slices [s0, s1) of part `part` of (row, kvh) ----
+  int row = -1, kvh = 0, s0 = 0, s1 = 0, part = 0, nparts = 0, kend = 0;
+  int64_t qs = 0, pidx = 0;
+  int d_first = -1;
   if (a.sched) {
+    // (row | parts << 16, kvh | part << 16, s0, s1), (query token, visible
+    // keys, physical block of slice s0 or -1, partial index)
     const int4* u = a.sched + 2 * (static_cast<int64_t>(blockIdx.x) * W + wave);
     const int4 u0 = u[0], u1 = u[1];
-    row = u0.x;
-    kvh = u0.y;
-    s0 = u0.z;
-    s1 = u0.w;
-    d_qs = u1.x;
-    d_kend = u1.y;
-    d_first = u1.z;
-    d_off = u1.w;
+    const int x = __builtin_amdgcn_readfirstlane(u0.x);
+    const int y = __builtin_amdgcn_readfirstlane(u0.y);
+    if (x >= 0) {
+      row = x & 0xffff;
+      nparts = (x >> 16) & 0xffff;
+      kvh = y & 0xffff;
+      part = (y >> 16) & 0xffff;
+    }
+    s0 = __builtin_amdgcn_readfirstlane(u0.z);
+    s1 = __builtin_amdgcn_readfirstlane(u0.w);
+    qs = __builtin_amdgcn_readfirstlane(u1.x);
+    kend = __builtin_amdgcn_readfirstlane(u1.y);
+    d_first = __builtin_amdgcn_readfirstlane(u1.z);
+    pidx = __builtin_amdgcn_readfirstlane(u1.w);
   } else {
     const int r = blockIdx.z;
     const int p = blockIdx.y;
     if (a.q_lens[r] != 1) return;
-    const int kend = decode_visible_keys(a, r);
-    if (p >= max((kend + PT - 1) / PT, 1)) return;
+    const int ke_r = decode_visible_keys(a, r);
+    const int np = max((ke_r + PT - 1) / PT, 1);
+    if (p >= np) return;
     const int kbeg = p * PT;
-    const int nsl = max((min(kend, kbeg + PT) - kbeg + 15) / 16, 0);
-    const int S = decode_splits(nsl, W, a.Hkv);
-    const int HW = W / S;
+    const int nsl = max((min(ke_r, kbeg + PT) - kbeg + 15) / 16, 0);
+    const int Sp = decode_splits(nsl, W, a.Hkv);
+    const int HW = W / Sp;
     if (static_cast<int>(blockIdx.x) * HW >= a.Hkv) return;
-    const int h = blockIdx.x * HW + wave / S;
-    const int split = wave % S;
+    const int h = blockIdx.x * HW + wave / Sp;
+    const int split = wave % Sp;
     if (h < a.Hkv) {
       row = r;
       kvh = h;
-      s0 = kbeg / 16 + (nsl * split) / S;
-      s1 = kbeg / 16 + (nsl * (split + 1)) / S;
+      s0 = kbeg / 16 + (nsl * split) / Sp;
+      s1 = kbeg / 16 + (nsl * (split + 1)) / Sp;
+      part = p;
+      nparts = np;
+      kend = ke_r;
+      qs = a.q_starts[r];
+      pidx = (static_cast<int64_t>(r) * a.Hkv + h) * a.max_parts + p;
     }
   }
   row = __builtin_amdgcn_readfirstlane(row);
   kvh = __builtin_amdgcn_readfirstlane(kvh);
   s0 = __builtin_amdgcn_readfirstlane(s0);
   s1 = __builtin_amdgcn_readfirstlane(s1);
-  bool valid;
-  int kend, off;
-  int64_t qs;
-  if (a.sched) {  // the descriptor carries the row's metadata: no dependent loads
-    valid = row >= 0 && kvh >= 0 && kvh < a.Hkv;
-    kend = __builtin_amdgcn_readfirstlane(d_kend);
-    kend = static_cast<int>(min(static_cast<int64_t>(kend), static_cast<int64_t>(a.max_parts) * PT));
-    qs = __builtin_amdgcn_readfirstlane(d_qs);
-    off = __builtin_amdgcn_readfirstlane(d_off);
-    d_first = __builtin_amdgcn_readfirstlane(d_first);
-  } else {
-    valid = row >= 0 && kvh >= 0 && kvh < a.Hkv && a.q_lens[row] == 1;
-    kend = valid ? decode_visible_keys(a, row) : 0;
-    qs = valid ? a.q_starts[row] : 0;
-    off = valid ? a.q_offs[row] : 0;
-  }
-  valid = valid && qs >= 0 && qs < a.total_q;
+  const bool valid = row >= 0 && kvh >= 0 && kvh < a.Hkv && qs >= 0 && qs < a.total_q && s0 >= 0 &&
+                     nparts >= 1 && part < nparts && (nparts == 1 || (pidx >= 0 && pidx < a.num_partials));
   const int kb = 16 * s0;
   const int ke = min(kend, 16 * s1);
+  const int nsl = valid && ke > kb ? (ke - kb + 15) / 16 : 0;
+
+  float* so = smem;                                      // [S][G][D]
+  float* sl = so + static_cast<int64_t>(S) * G * D;      // [S][G]
+  int* skey = reinterpret_cast<int*>(sl + S * G);        // [S][4] row, kvh, part, -
+  int* cnt = skey + 4 * S;                               // [W] next slice to claim
+  int* dend = cnt + W;                                   // [W] end of the range
+  int* info = dend + W;                                  // [W][kDecInfo]
+  int* nslot = info + kDecInfo * W;                      // slots handed out
+
+  const int bs = a.bs;
+  auto block_of = [&](int r, int slice) -> int64_t {     // physical block of a slice
+    const int64_t lb = (16 * static_cast<int64_t>(slice)) / bs;
+    int64_t id = lb < a.bt_stride ? a.bt[static_cast<int64_t>(r) * a.bt_stride + lb] : 0;
+    return id < 0 ? 0 : (id >= a.num_blocks ? a.num_blocks - 1 : id);
+  };
+
+  // The current segment (starts as this wave's own).  A decode row's causal
+  // limit is already in kend (its one query sees keys [0, kend)), so the
+  // query position passed to the m-row setup is kend - 1.
+  int krow = valid ? row : -1, kkvh = kvh, kpart = part, kkend = kend;
 
   WaveAttn<TT, D, 1, false> wa;
-  wa.setup(a, lane, valid ? kvh : 0, qs, 0, valid ? 1 : 0, off);
-  if (valid && ke > kb) wa.attend(a, row, kvh, kb, ke, a.causal ? off : INT_MAX, d_first);
-  float ltot[1];
-  wa.row_sums(ltot);
-
-  float* so = smem;                                    // [W][G][D]
-  float* sl = smem + W * G * D;                        // [W][G]
-  int* sk = reinterpret_cast<int*>(sl + W * G);        // [W][4] (row, kvh, partition, parts)
-  int64_t* sq = reinterpret_cast<int64_t*>(sk + 4 * W); // [W] query token
-  if (wa.mval[0]) {
-    const float inv = ltot[0] > 0.f ? 1.f / ltot[0] : 0.f;
-    float* dst = so + (wave * G + wa.n) * D;
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-#pragma unroll
-      for (int e = 0; e < D / 16; e += 4)
-        *reinterpret_cast<f32x4*>(dst + (D / 16) * (4 * wa.g + j) + e) =
-            f32x4{wa.o[0][e][j] * inv, wa.o[0][e + 1][j] * inv, wa.o[0][e + 2][j] * inv,
-                  wa.o[0][e + 3][j] * inv};
-    if (wa.g == 0) sl[wave * G + wa.n] = ltot[0] > 0.f ? wa.m[0] + __log2f(ltot[0]) : -INFINITY;
-  }
+  wa.setup(a, lane, valid ? kvh : 0, qs, 0, valid ? 1 : 0, kend - 1);
+  KVSlice<D> T;
+  int i = s0;              // slice whose loads are in flight, if `have`
+  bool have = nsl > 0;     // the first slice of the range is taken without a claim
+  if (have)
+    wa.load_slice(a, kvh, d_first >= 0 ? min(static_cast<int64_t>(d_first), a.num_blocks - 1) : block_of(row, s0),
+                  kb % bs, T);
   if (lane == 0) {
-    sk[4 * wave + 0] = valid ? row : -1;
-    sk[4 * wave + 1] = kvh;
-    sk[4 * wave + 2] = kb / PT;
-    sk[4 * wave + 3] = valid ? max((kend + PT - 1) / PT, 1) : 0;
-    sq[wave] = qs;
+    cnt[wave] = s0 + (have ? 1 : 0);
+    dend[wave] = s0 + nsl;
+    int* d = info + kDecInfo * wave;
+    d[0] = krow; d[1] = kvh; d[2] = part; d[3] = nparts;
+    d[4] = static_cast<int>(qs); d[5] = kend; d[6] = 0; d[7] = 0;
+    skey[4 * wave] = -1;
+    if (wave == 0) *nslot = W;
+  }
+  // LDS-only barrier: the first slice's loads stay in flight across it.
+  __asm__ volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+
+  // Claims one slice of range v (-1 when the range is used up).
+  auto claim = [&](int v) -> int {
+    int r = 0;
+    if (lane == 0) r = atomicAdd(&cnt[v], 1);
+    r = __builtin_amdgcn_readlane(r, 0);
+    return r < __builtin_amdgcn_readfirstlane(dend[v]) ? r : -1;
+  };
+  // Range with the most slices left (only ranges of the current segment when
+  // same_segment), or -1.
+  auto pick = [&](bool same_segment) -> int {
+    int best = -1;
+    if (lane < W) {
+      const int left = dend[lane] - cnt[lane];
+      const int* d = info + kDecInfo * lane;
+      bool ok = left > 0;
+      if (same_segment) ok = ok && d[0] == krow && d[1] == kkvh && d[2] == kpart;
+      best = ok ? (min(left, 1 << 24) << 6) | lane : -1;
+    }
+    best = wave_max_int(best);
+    return best < 0 ? -1 : (best & 63);
+  };
+  int slot = wave;
+  bool used = false;       // the slot holds work
+  auto flush = [&]() {
+    float lt[1];
+    wa.row_sums(lt);
+    if (wa.mval[0]) {
+      const float inv = lt[0] > 0.f ? 1.f / lt[0] : 0.f;
+      float* dst = so + (static_cast<int64_t>(slot) * G + wa.n) * D;
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int e = 0; e < D / 16; e += 4)
+          *reinterpret_cast<f32x4*>(dst + (D / 16) * (4 * wa.g + j) + e) =
+              f32x4{wa.o[0][e][j] * inv, wa.o[0][e + 1][j] * inv, wa.o[0][e + 2][j] * inv,
+                    wa.o[0][e + 3][j] * inv};
+      if (wa.g == 0) sl[slot * G + wa.n] = lt[0] > 0.f ? wa.m[0] + __log2f(lt[0]) : -INFINITY;
+    }
+    if (lane == 0) {
+      skey[4 * slot + 0] = krow;
+      skey[4 * slot + 1] = kkvh;
+      skey[4 * slot + 2] = kpart;
+      skey[4 * slot + 3] = 0;
+    }
+  };
+
+  int cv = wave;           // range being claimed from
+  bool live = nsl > 0;     // the current segment may still have slices
+  for (;;) {
+    int j = -1;
+    if (live) {
+      j = claim(cv);
+      while (j < 0) {
+        const int v = pick(true);
+        if (v < 0) break;
+        cv = v;
+        j = claim(cv);
+      }
+      live = j >= 0;
+    }
+    // The next slice's block id is fetched while this slice's loads land.
+    const int64_t jb = j >= 0 ? block_of(krow, j) : 0;
+    if (have) {
+      wa.compute_slice(a, 16 * i, kkend, INT_MAX, T);
+      used = true;
+    }
+    if (j >= 0) {
+      i = j;
+      wa.load_slice(a, kkvh, jb, (16 * j) % bs, T);
+      have = true;
+      continue;
+    }
+    have = false;
+    // Segment exhausted: park its state, then take slices of another one.
+    if (used) flush();
+    const int v = pick(false);
+    if (v < 0) break;
+    if (used) {
+      int ns = 0;
+      if (lane == 0) ns = atomicAdd(nslot, 1);
+      ns = __builtin_amdgcn_readlane(ns, 0);
+      if (ns >= S) break;
+      slot = ns;
+      if (lane == 0) skey[4 * slot] = -1;
+      used = false;
+    }
+    const int* d = info + kDecInfo * v;
+    krow = __builtin_amdgcn_readfirstlane(d[0]);
+    kkvh = __builtin_amdgcn_readfirstlane(d[1]);
+    kpart = __builtin_amdgcn_readfirstlane(d[2]);
+    kkend = __builtin_amdgcn_readfirstlane(d[5]);
+    wa.setup(a, lane, kkvh, __builtin_amdgcn_readfirstlane(d[4]), 0, 1, kkend - 1);
+    cv = v;
+    live = true;
   }
   __syncthreads();
 
-  // ---- merge every segment (maximal run of waves with one key) ----
-  auto same = [&](int x, int y) {
-    return sk[4 * x] == sk[4 * y] && sk[4 * x + 1] == sk[4 * y + 1] && sk[4 * x + 2] == sk[4 * y + 2];
-  };
-  for (int w0 = 0; w0 < W; ++w0) {
-    if (sk[4 * w0] < 0 || (w0 > 0 && same(w0 - 1, w0))) continue;
-    int w1 = w0 + 1;
-    while (w1 < W && same(w0, w1)) ++w1;
-    const int srow = sk[4 * w0], skvh = sk[4 * w0 + 1], sp = sk[4 * w0 + 2], snp = sk[4 * w0 + 3];
-    const int64_t sqs = sq[w0];
-    for (int it = threadIdx.x; it < G * (D / 4); it += 64 * W) {
-      const int hh = it / (D / 4);
-      const int d0 = 4 * (it % (D / 4));
-      float mx = -INFINITY;
-      for (int w = w0; w < w1; ++w) mx = fmaxf(mx, sl[w * G + hh]);
-      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-      float lsum = 0.f;
-      if (mx != -INFINITY) {
-        for (int w = w0; w < w1; ++w) {
-          const float wt = fast_exp2(sl[w * G + hh] - mx);
-          lsum += wt;
-          acc += wt * *reinterpret_cast<const f32x4*>(so + (w * G + hh) * D + d0);
-        }
+  // ---- merge: the first wave of each segment combines the segment's slots ----
+  if (!valid) return;
+  if (wave > 0) {
+    const int* d = info + kDecInfo * (wave - 1);
+    if (d[0] == row && d[1] == kvh && d[2] == part) return;
+  }
+  const int nused = min(__builtin_amdgcn_readfirstlane(*nslot), S);
+  const bool mine = lane < nused && skey[4 * lane] == row && skey[4 * lane + 1] == kvh &&
+                    skey[4 * lane + 2] == part;
+  const uint64_t slots = __ballot(mine);
+  for (int it = lane; it < G * (D / 4); it += 64) {
+    const int hh = it / (D / 4);
+    const int d0 = 4 * (it % (D / 4));
+    float mx = -INFINITY;
+    for (uint64_t b = slots; b; b &= b - 1) mx = fmaxf(mx, sl[__builtin_ctzll(b) * G + hh]);
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    float lsum = 0.f;
+    if (mx != -INFINITY) {
+      for (uint64_t b = slots; b; b &= b - 1) {
+        const int w = __builtin_ctzll(b);
+        const float wt = fast_exp2(sl[w * G + hh] - mx);
+        lsum += wt;
+        acc += wt * *reinterpret_cast<const f32x4*>(so + (static_cast<int64_t>(w) * G + hh) * D + d0);
       }
-      const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
-      const int h = skvh * G + hh;
-      const float lse2 = lsum > 0.f ? mx + __log2f(lsum) : -INFINITY;
-      if (snp == 1) {
-        st* dp = static_cast<st*>(a.o) + sqs * a.o_st + static_cast<int64_t>(h) * a.o_sh + d0;
-        *reinterpret_cast<u32x2*>(dp) =
-            u32x2{TT::pack2(acc.x * inv, acc.y * inv), TT::pack2(acc.z * inv, acc.w * inv)};
-        if (a.lse && d0 == 0) a.lse[sqs * a.l_st + static_cast<int64_t>(h) * a.l_sh] = lse2 * kLn2;
-      } else {
-        const int64_t pidx = (static_cast<int64_t>(srow) * a.Hq + h) * a.max_parts + sp;
-        *reinterpret_cast<f32x4*>(a.ws_o + pidx * D + d0) = acc * inv;
-        if (d0 == 0) a.ws_lse[pidx] = lse2;
-      }
+    }
+    const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
+    const int h = kvh * G + hh;
+    const float lse2 = lsum > 0.f ? mx + __log2f(lsum) : -INFINITY;
+    if (nparts == 1) {
+      st* dp = static_cast<st*>(a.o) + qs * a.o_st + static_cast<int64_t>(h) * a.o_sh + d0;
+      *reinterpret_cast<u32x2*>(dp) =
+          u32x2{TT::pack2(acc.x * inv, acc.y * inv), TT::pack2(acc.z * inv, acc.w * inv)};
+      if (a.lse && d0 == 0) a.lse[qs * a.l_st + static_cast<int64_t>(h) * a.l_sh] = lse2 * kLn2;
+    } else {
+      *reinterpret_cast<f32x4*>(a.ws_o + (pidx * G + hh) * D + d0) = acc * inv;
+      if (d0 == 0) a.ws_lse[pidx * G + hh] = lse2;
     }
   }
 }
 
-// Combines the per-work-group partitions of decode rows: one lane per (row,
-// query head, 8 head_dim values).  Rows finished by a single partition are
-// skipped; the partition count is recomputed exactly as the decode kernel did.
+// Combines the parts of split decode segments: (row, kv head) pieces that
+// ran in different work-groups and left (LSE, O) partials.  With a schedule,
+// work-group u takes merge unit u = (query token, kv head, parts, first
+// partial index), each lane 8 head_dim values of one of the G query heads.
+// Without one, the grid is (head_dim chunks, rows), and a row's parts are the
+// fixed partitions of part_tokens keys, recomputed as the decode kernel did.
 template <class TT, int D>
-__global__ void __launch_bounds__(256)
+__global__ void __launch_bounds__(64)
 attn_merge_kernel(const AttnArgs a) {
   using st = uint16_t;
   constexpr int CH = D / 8;
-  const int row = blockIdx.y;
-  if (a.q_lens[row] != 1) return;
-  const int idx = blockIdx.x * 256 + threadIdx.x;
-  if (idx >= a.Hq * CH) return;
-  const int h = idx / CH;
-  const int c = idx % CH;
-  const int PT = a.part_tokens;
-  const int nparts = (decode_visible_keys(a, row) + PT - 1) / PT;
-  if (nparts <= 1) return;
-  const int64_t t = a.q_starts[row];
-  if (t < 0 || t >= a.total_q) return;
-
-  const int64_t base = (static_cast<int64_t>(row) * a.Hq + h) * a.max_parts;
-  float mmax = -INFINITY;
-  for (int pp = 0; pp < nparts; ++pp) mmax = fmaxf(mmax, a.ws_lse[base + pp]);
-  f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
-  float lsum = 0.f;
-  if (mmax != -INFINITY) {
-    for (int pp = 0; pp < nparts; ++pp) {
-      const float w = fast_exp2(a.ws_lse[base + pp] - mmax);
-      lsum += w;
-      const f32x4* src = reinterpret_cast<const f32x4*>(a.ws_o + (base + pp) * D + 8 * c);
-      acc0 += w * src[0];
-      acc1 += w * src[1];
-    }
+  const int G = a.G;
+  int64_t t, base;
+  int kvh, nparts, it0, step;
+  if (a.merge_units) {
+    const int4 u = a.merge_units[2 * static_cast<int64_t>(blockIdx.x)];
+    t = u.x;
+    kvh = u.y;
+    nparts = u.z;
+    base = u.w;
+    it0 = threadIdx.x;
+    step = 64;
+  } else {
+    const int row = blockIdx.y;
+    if (a.q_lens[row] != 1) return;
+    const int idx = blockIdx.x * 64 + threadIdx.x;
+    if (idx >= a.Hq * CH) return;
+    const int PT = a.part_tokens;
+    nparts = (decode_visible_keys(a, row) + PT - 1) / PT;
+    if (nparts <= 1) return;
+    t = a.q_starts[row];
+    kvh = (idx / CH) / G;
+    base = (static_cast<int64_t>(row) * a.Hkv + kvh) * a.max_parts;
+    it0 = idx - kvh * G * CH;  // (head in group, chunk) of this lane
+    step = G * CH;             // one item per lane
   }
-  const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
-  st* dp = static_cast<st*>(a.o) + t * a.o_st + static_cast<int64_t>(h) * a.o_sh + 8 * c;
-  *reinterpret_cast<u32x4*>(dp) =
-      u32x4{TT::pack2(acc0.x * inv, acc0.y * inv), TT::pack2(acc0.z * inv, acc0.w * inv),
-            TT::pack2(acc1.x * inv, acc1.y * inv), TT::pack2(acc1.z * inv, acc1.w * inv)};
-  if (a.lse && c == 0)
-    a.lse[t * a.l_st + static_cast<int64_t>(h) * a.l_sh] =
-        lsum > 0.f ? (mmax + __log2f(lsum)) * kLn2 : -INFINITY;
+  if (t < 0 || t >= a.total_q || kvh < 0 || kvh >= a.Hkv || nparts < 1 || base < 0 ||
+      base + nparts > a.num_partials)
+    return;
+  constexpr int kFew = 4;  // up to this many parts, every load is issued at once
+  for (int it = it0; it < G * CH; it += step) {
+    const int hh = it / CH;
+    const int c = it % CH;
+    float mmax = -INFINITY;
+    f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+    float lsum = 0.f;
+    if (nparts <= kFew) {
+      float lv[kFew];
+      f32x4 p0[kFew], p1[kFew];
+#pragma unroll
+      for (int pp = 0; pp < kFew; ++pp) {
+        lv[pp] = -INFINITY;
+        p0[pp] = p1[pp] = f32x4{0.f, 0.f, 0.f, 0.f};
+        if (pp < nparts) {
+          lv[pp] = a.ws_lse[(base + pp) * G + hh];
+          const f32x4* src = reinterpret_cast<const f32x4*>(a.ws_o + ((base + pp) * G + hh) * D + 8 * c);
+          p0[pp] = src[0];
+          p1[pp] = src[1];
+        }
+      }
+#pragma unroll
+      for (int pp = 0; pp < kFew; ++pp) mmax = fmaxf(mmax, lv[pp]);
+      if (mmax != -INFINITY) {
+#pragma unroll
+        for (int pp = 0; pp < kFew; ++pp) {
+          const float w = pp < nparts ? fast_exp2(lv[pp] - mmax) : 0.f;
+          lsum += w;
+          acc0 += w * p0[pp];
+          acc1 += w * p1[pp];
+        }
+      }
+    } else {
+      for (int pp = 0; pp < nparts; ++pp) mmax = fmaxf(mmax, a.ws_lse[(base + pp) * G + hh]);
+      if (mmax != -INFINITY) {
+        for (int pp = 0; pp < nparts; ++pp) {
+          const float w = fast_exp2(a.ws_lse[(base + pp) * G + hh] - mmax);
+          lsum += w;
+          const f32x4* src = reinterpret_cast<const f32x4*>(a.ws_o + ((base + pp) * G + hh) * D + 8 * c);
+          acc0 += w * src[0];
+          acc1 += w * src[1];
+        }
+      }
+    }
+    const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
+    const int h = kvh * G + hh;
+    st* dp = static_cast<st*>(a.o) + t * a.o_st + static_cast<int64_t>(h) * a.o_sh + 8 * c;
+    *reinterpret_cast<u32x4*>(dp) =
+        u32x4{TT::pack2(acc0.x * inv, acc0.y * inv), TT::pack2(acc0.z * inv, acc0.w * inv),
+              TT::pack2(acc1.x * inv, acc1.y * inv), TT::pack2(acc1.z * inv, acc1.w * inv)};
+    if (a.lse && c == 0)
+      a.lse[t * a.l_st + static_cast<int64_t>(h) * a.l_sh] =
+          lsum > 0.f ? (mmax + __log2f(lsum)) * kLn2 : -INFINITY;
+  }
 }
 
 // -------------------------------------------------------------- prefill --
@@ -709,40 +874,40 @@ attn_generic_kernel(const AttnArgs a) {
 // ------------------------------------------------------------------ host --
 
 constexpr int64_t kMaxLdsBytes = 64 * 1024;
-#ifndef KVHOT_MIN_SLICES_PER_WAVE
-#define KVHOT_MIN_SLICES_PER_WAVE 8
-#endif
-#ifndef KVHOT_DECODE_ROUNDS
-#define KVHOT_DECODE_ROUNDS 1
-#endif
 #ifndef KVHOT_MAX_DECODE_WAVES
 #define KVHOT_MAX_DECODE_WAVES 16
 #endif
-// Lower bound on the planner's slices per wave: shorter chains cost more in
-// per-wave setup and merge than they save.
-constexpr int64_t kMinSlicesPerWave = KVHOT_MIN_SLICES_PER_WAVE;
-// Device-fulls of decode work-groups the planner aims for.
-constexpr int64_t kDecodeRounds = KVHOT_DECODE_ROUNDS;
 
 // Waves per decode work-group: 16 (head_dim <= 128, whose registers allow 4
-// waves per SIMD) when its LDS fits, else 8, else 0 (no MFMA path).
+// waves per SIMD) when one slot per wave fits in LDS, else 8, else 0 (no MFMA
+// path).
 static int decode_waves(int64_t G, int64_t D) {
-  if (KVHOT_MAX_DECODE_WAVES >= 16 && D <= 128 && decode_lds_floats(16, G, D) * 4 <= kMaxLdsBytes)
+  if (KVHOT_MAX_DECODE_WAVES >= 16 && D <= 128 && decode_lds_words(16, 16, G, D) * 4 <= kMaxLdsBytes)
     return 16;
-  if (decode_lds_floats(8, G, D) * 4 <= kMaxLdsBytes) return 8;
+  if (decode_lds_words(8, 8, G, D) * 4 <= kMaxLdsBytes) return 8;
   return 0;
 }
 
-struct Plan {
-  bool mfma = false;
-  int waves = 0;        // waves per decode work-group
-  int part_tokens = 0;  // keys per decode partition
-  int max_parts = 1;
-  int64_t lse_bytes = 0, o_bytes = 0;
-  int64_t workspace_bytes() const { return lse_bytes + o_bytes; }
-};
+// LDS slots of a decode work-group of W waves: one per wave plus a pool of up
+// to W more for waves that move on to other segments, as LDS allows.
+static int decode_slots(int W, int64_t G, int64_t D) {
+  const int64_t spare = kMaxLdsBytes / 4 - decode_lds_words(W, W, G, D);
+  const int64_t per_slot = G * D + G + 4;
+  return W + static_cast<int>(std::max<int64_t>(0, std::min<int64_t>(W, spare / per_slot)));
+}
 
-static int64_t round_up(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
+// Bytes of one split-K partial: the normalised O and LSE of G query heads.
+static int64_t partial_bytes(int64_t G, int64_t D) { return G * (D + 1) * 4; }
+
+struct Plan {
+  bool mfma = false;     // the MFMA kernels take this shape
+  bool grid_ok = false;  // ... also without a schedule (partition count fits the grid)
+  int waves = 0;         // waves per decode work-group
+  int part_tokens = 0;   // keys per decode partition (no schedule)
+  int max_parts = 1;
+  int64_t partials = 0;  // split-K partials without a schedule
+  int64_t workspace_bytes(int64_t G, int64_t D) const { return partials * partial_bytes(G, D); }
+};
 
 static bool mfma_shape_ok(int64_t Hq, int64_t Hkv, int64_t D, int64_t bs, int dtype) {
   if (dtype != KVHOT_BF16 && dtype != KVHOT_F16) return false;
@@ -753,27 +918,23 @@ static bool mfma_shape_ok(int64_t Hq, int64_t Hkv, int64_t D, int64_t bs, int dt
   return decode_waves(G, D) > 0;
 }
 
-// part_tokens = 0: grid-mode default of W * KVHOT_SLICES_PER_WAVE slices, so
-// no wave walks more than that many; a host schedule passes its own size.
+// Without a schedule, decode rows are cut into partitions of part_tokens keys
+// (0: W * KVHOT_SLICES_PER_WAVE slices, so no wave walks more than that many)
+// and the grid enumerates (head group, partition, row).
 static Plan make_plan(int64_t rows, int64_t max_q, int64_t max_k, int64_t Hq,
                       int64_t Hkv, int64_t D, int64_t bs, int64_t part_tokens,
                       int dtype) {
   Plan pl;
   pl.mfma = mfma_shape_ok(Hq, Hkv, D, bs, dtype);
-  if (!pl.mfma || max_q < 1 || max_k < 1) return pl;
+  if (!pl.mfma || max_q < 1) return pl;
   pl.waves = decode_waves(Hq / Hkv, D);
   pl.part_tokens = part_tokens > 0 ? static_cast<int>(part_tokens)
                                    : 16 * pl.waves * KVHOT_SLICES_PER_WAVE;
-  const int64_t parts = (max_k + pl.part_tokens - 1) / pl.part_tokens;
-  if (parts > 65535) {
-    pl.mfma = false;
-    return pl;
-  }
+  const int64_t parts = std::max<int64_t>((max_k + pl.part_tokens - 1) / pl.part_tokens, 1);
+  if (parts > 65535) return pl;
+  pl.grid_ok = true;
   pl.max_parts = static_cast<int>(parts);
-  if (pl.max_parts > 1) {
-    pl.lse_bytes = round_up(rows * Hq * pl.max_parts * 4, 256);
-    pl.o_bytes = rows * Hq * pl.max_parts * D * 4;
-  }
+  if (pl.max_parts > 1) pl.partials = rows * Hkv * pl.max_parts;
   return pl;
 }
 
@@ -784,7 +945,7 @@ constexpr int prefill_nm(int64_t D) { return D <= 128 ? 4 : 2; }
 template <class TT, int D, int W>
 static int decode_groups_per_cu(int64_t G) {
   int n = 0;
-  const size_t lds = static_cast<size_t>(decode_lds_floats(W, G, D) * 4);
+  const size_t lds = static_cast<size_t>(decode_lds_words(W, decode_slots(W, G, D), G, D) * 4);
   if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, attn_decode_kernel<TT, D, W>, 64 * W, lds) !=
       hipSuccess)
     n = 0;
@@ -795,8 +956,7 @@ template <class TT>
 static int decode_groups_per_cu(int64_t D, int W, int64_t G) {
   if (W == 16) {
     if (D == 64) return decode_groups_per_cu<TT, 64, 16>(G);
-    if (D == 128) return decode_groups_per_cu<TT, 128, 16>(G);
-    return decode_groups_per_cu<TT, 256, 16>(G);
+    return decode_groups_per_cu<TT, 128, 16>(G);
   }
   if (D == 64) return decode_groups_per_cu<TT, 64, 8>(G);
   if (D == 128) return decode_groups_per_cu<TT, 128, 8>(G);
@@ -817,109 +977,146 @@ static int64_t resident_decode_waves(int dtype, int64_t D, int W, int64_t G) {
   return static_cast<int64_t>(cus) * per * W;
 }
 
-struct Segment {
-  int row, kvh, s0, s1, waves;
+struct Piece {
+  int row, kvh, s0, s1, part, seg;
 };
 
-// Decode launch list: every (row, kv head, partition) segment of n slices
-// gets ceil(n / T) <= W waves, segments are packed best-fit-decreasing into
-// W-wave work-groups, and T is the smallest value >= kMinSlicesPerWave whose
-// packing fits on the device at once (so every wave walks <= T slices and
-// all of them run concurrently).  Returns the partition size used.
-static int64_t plan_decode(const int32_t* q_lens, const int32_t* k_lens, const int32_t* q_offs,
-                           const int32_t* q_starts, const int32_t* bt, int64_t bt_stride,
-                           int64_t bs, int64_t rows, int64_t Hkv, bool causal, int W,
-                           int64_t resident, int64_t given_pt, std::vector<int4>& out) {
+// Minimum slices per decode work-group: below it, a split costs more (partial
+// stores and a merge) than the parallelism gains.
+constexpr int64_t kMinGroupSlicesPerWave = 2;
+// Split pieces shorter than this are not cut off a segment.
+constexpr int64_t kMinPieceSlices = 4;
+
+// Decode launch list.  Work-groups of one device-full are given equal numbers
+// of 16-token slices (inside a work-group the waves balance themselves by
+// claiming slices, so only the per-work-group total matters): the (row, kv
+// head) segments are laid end to end and cut every `target` slices, a
+// segment that straddles a cut becoming parts in several work-groups (joined
+// by attn_merge_kernel).  A work-group holds at most W pieces.  Its waves are
+// shared among its pieces in proportion to their slices, and each wave's
+// starting range is an even share of its piece.  With given_pt > 0 segments
+// are first cut at multiples of given_pt keys and those partitions are never
+// split further.
+//
+// Per wave two int4: (row | parts << 16, kvh | part << 16, first slice, end
+// slice) and (query token, visible keys, physical block of the first slice
+// or -1, partial index).  Per split segment two int4: (query token, kv head,
+// parts, first partial index) and zeros.  Returns false when a count does not
+// fit its 16-bit field.
+static bool plan_decode(const int32_t* q_lens, const int32_t* k_lens, const int32_t* q_offs,
+                        const int32_t* q_starts, const int32_t* bt, int64_t bt_stride, int64_t bs,
+                        int64_t rows, int64_t Hkv, bool causal, int W, int64_t groups,
+                        int64_t given_pt, std::vector<int4>& dec, std::vector<int4>& mrg,
+                        int64_t& partials) {
+  dec.clear();
+  mrg.clear();
+  partials = 0;
   std::vector<int64_t> kend(rows, -1);
   int64_t total = 0;
   for (int64_t r = 0; r < rows; ++r) {
     if (q_lens[r] != 1) continue;
     const int64_t klen = k_lens[r], off = q_offs[r];
     kend[r] = std::max<int64_t>(causal ? std::min(klen, off + 1) : klen, 0);
-    total += std::max<int64_t>((kend[r] + 15) / 16, 1) * Hkv;
+    total += (kend[r] + 15) / 16 * Hkv;
   }
-  std::vector<Segment> segs;
-  std::vector<std::vector<int>> groups;  // segment indices per work-group
-  auto build = [&](int64_t T, int64_t PT) {
-    segs.clear();
-    groups.clear();
-    for (int64_t r = 0; r < rows; ++r) {
-      if (kend[r] < 0) continue;
-      const int64_t nparts = std::max<int64_t>((kend[r] + PT - 1) / PT, 1);
-      for (int64_t p = 0; p < nparts; ++p) {
-        const int64_t kb = p * PT, ke = std::min(kend[r], kb + PT);
-        const int64_t n = std::max<int64_t>((ke - kb + 15) / 16, 0);
-        const int w = static_cast<int>(std::min<int64_t>(std::max<int64_t>((n + T - 1) / T, 1), W));
-        for (int64_t h = 0; h < Hkv; ++h)
-          segs.push_back(Segment{static_cast<int>(r), static_cast<int>(h), static_cast<int>(kb / 16),
-                                 static_cast<int>(kb / 16 + n), w});
-      }
-    }
-    std::vector<int> order(segs.size());
-    for (size_t i = 0; i < order.size(); ++i) order[i] = static_cast<int>(i);
-    std::stable_sort(order.begin(), order.end(),
-                     [&](int x, int y) { return segs[x].waves > segs[y].waves; });
-    std::vector<std::vector<int>> by_free(W + 1);  // work-groups by free slots
-    std::vector<int> free_slots;
-    for (int si : order) {
-      const int w = segs[si].waves;
-      int f = w;
-      while (f <= W && by_free[f].empty()) ++f;
-      int gi;
-      if (f > W || f == W) {  // no partly used group fits: open a new one
-        gi = static_cast<int>(groups.size());
-        groups.emplace_back();
-        free_slots.push_back(W);
-        f = W;
-        if (!by_free[W].empty() && by_free[W].back() == gi) by_free[W].pop_back();
-      } else {
-        gi = by_free[f].back();
-        by_free[f].pop_back();
-      }
-      groups[gi].push_back(si);
-      free_slots[gi] = f - w;
-      if (free_slots[gi] > 0) by_free[free_slots[gi]].push_back(gi);
-    }
+  const int64_t target = std::max<int64_t>((total + std::max<int64_t>(groups, 1) - 1) / std::max<int64_t>(groups, 1),
+                                           kMinGroupSlicesPerWave * W);
+  const int64_t slack = std::max<int64_t>(2, target / 32);
+
+  std::vector<std::vector<Piece>> wgs;
+  std::vector<Piece> cur;
+  int64_t load = 0;
+  auto close = [&]() {
+    if (!cur.empty()) wgs.push_back(cur);
+    cur.clear();
+    load = 0;
   };
-  int64_t T, PT;
-  if (given_pt > 0) {
-    PT = given_pt;
-    T = std::max<int64_t>((PT / 16 + W - 1) / W, 1);
-    build(T, PT);
-  } else {
-    const int64_t target = std::max<int64_t>(resident, 1) * kDecodeRounds;
-    T = std::max<int64_t>(kMinSlicesPerWave, (total + target - 1) / target);
-    for (;;) {
-      PT = 16 * W * T;
-      build(T, PT);
-      if (static_cast<int64_t>(groups.size()) * W <= target || T >= (1 << 16)) break;
-      T += std::max<int64_t>(1, T / 8);
-    }
-  }
-  // Two int4 per wave: (row, kv head, first slice, end slice) and (query
-  // token, visible keys, physical block of the first slice or -1, query
-  // position) -- everything a wave needs before its first K/V load.
-  out.clear();
-  for (const auto& g : groups) {
-    int used = 0;
-    for (int si : g) {
-      const Segment& sg = segs[si];
-      const int n = sg.s1 - sg.s0;
-      for (int i = 0; i < sg.waves; ++i) {
-        const int a0 = sg.s0 + (n * i) / sg.waves, a1 = sg.s0 + (n * (i + 1)) / sg.waves;
-        const int64_t lb = 16 * static_cast<int64_t>(a0) / bs;
-        const int first = lb < bt_stride ? bt[sg.row * bt_stride + lb] : -1;
-        out.push_back(int4{sg.row, sg.kvh, a0, a1});
-        out.push_back(int4{q_starts[sg.row], static_cast<int>(kend[sg.row]), first, q_offs[sg.row]});
+  std::vector<int> seg_parts;  // parts per segment (row, kv head)
+  std::vector<int> seg_row, seg_kvh;
+  for (int64_t r = 0; r < rows; ++r) {
+    if (kend[r] < 0) continue;
+    const int64_t n = (kend[r] + 15) / 16;
+    const int64_t pt_sl = given_pt > 0 ? given_pt / 16 : 0;
+    for (int64_t h = 0; h < Hkv; ++h) {
+      const int seg = static_cast<int>(seg_parts.size());
+      seg_parts.push_back(0);
+      seg_row.push_back(static_cast<int>(r));
+      seg_kvh.push_back(static_cast<int>(h));
+      // Atoms: the fixed partitions, or the whole segment (splittable).
+      const int64_t natoms = pt_sl > 0 ? std::max<int64_t>((n + pt_sl - 1) / pt_sl, 1) : 1;
+      for (int64_t p = 0; p < natoms; ++p) {
+        int64_t s = pt_sl > 0 ? p * pt_sl : 0;
+        int64_t rem = (pt_sl > 0 ? std::min(n, s + pt_sl) : n) - s;
+        const bool splittable = pt_sl == 0;
+        for (;;) {
+          if (static_cast<int>(cur.size()) == W) close();
+          const int64_t space = target - load;
+          if (rem <= space + slack || (!splittable && cur.empty())) {
+            const int part = splittable ? seg_parts[seg]++ : static_cast<int>(p);
+            cur.push_back(Piece{static_cast<int>(r), static_cast<int>(h), static_cast<int>(s),
+                                static_cast<int>(s + rem), part, seg});
+            load += rem;
+            break;
+          }
+          if (!splittable || space < kMinPieceSlices) {
+            close();
+            continue;
+          }
+          int64_t take = space;
+          if (rem - take < kMinPieceSlices) take = rem - kMinPieceSlices;
+          cur.push_back(Piece{static_cast<int>(r), static_cast<int>(h), static_cast<int>(s),
+                              static_cast<int>(s + take), seg_parts[seg]++, seg});
+          s += take;
+          rem -= take;
+          close();
+        }
       }
-      used += sg.waves;
-    }
-    for (; used < W; ++used) {
-      out.push_back(int4{-1, 0, 0, 0});
-      out.push_back(int4{0, 0, -1, 0});
+      if (pt_sl > 0) seg_parts[seg] = static_cast<int>(natoms);
     }
   }
-  return PT;
+  close();
+
+  // Partial indices of split segments.
+  std::vector<int64_t> seg_base(seg_parts.size(), -1);
+  for (size_t sg = 0; sg < seg_parts.size(); ++sg) {
+    if (seg_parts[sg] > 65535) return false;
+    if (seg_parts[sg] > 1) {
+      seg_base[sg] = partials;
+      mrg.push_back(int4{q_starts[seg_row[sg]], seg_kvh[sg], seg_parts[sg], static_cast<int>(partials)});
+      mrg.push_back(int4{0, 0, 0, 0});
+      partials += seg_parts[sg];
+      if (partials > 0x7fffffff) return false;
+    }
+  }
+
+  for (const auto& g : wgs) {
+    // Waves per piece: one each, the rest to the piece with most slices per wave.
+    const int k = static_cast<int>(g.size());
+    std::vector<int> w(k, 1);
+    for (int extra = W - k; extra > 0; --extra) {
+      int best = 0;
+      for (int i = 1; i < k; ++i)
+        if (static_cast<int64_t>(g[i].s1 - g[i].s0) * w[best] > static_cast<int64_t>(g[best].s1 - g[best].s0) * w[i])
+          best = i;
+      ++w[best];
+    }
+    for (int i = 0; i < k; ++i) {
+      const Piece& pc = g[i];
+      const int nparts = seg_parts[pc.seg];
+      const int n = pc.s1 - pc.s0;
+      const int r = pc.row;
+      const int pidx = nparts > 1 ? static_cast<int>(seg_base[pc.seg] + pc.part) : 0;
+      for (int j = 0; j < w[i]; ++j) {
+        const int a0 = pc.s0 + static_cast<int>((static_cast<int64_t>(n) * j) / w[i]);
+        const int a1 = pc.s0 + static_cast<int>((static_cast<int64_t>(n) * (j + 1)) / w[i]);
+        const int64_t lb = 16 * static_cast<int64_t>(a0) / bs;
+        const int first = (a0 < a1 && lb < bt_stride) ? bt[r * bt_stride + lb] : -1;
+        dec.push_back(int4{r | (nparts << 16), pc.kvh | (pc.part << 16), a0, a1});
+        dec.push_back(int4{q_starts[r], static_cast<int>(kend[r]), first, pidx});
+      }
+    }
+  }
+  return true;
 }
 
 // Prefill launch list: (row, kv head, query block) units, longest key range first.
@@ -954,22 +1151,28 @@ static void launch_decode(const AttnArgs& a, int64_t rows, int64_t n_dec, hipStr
   dim3 grid = a.sched ? dim3(static_cast<uint32_t>(n_dec / W))
                       : dim3(static_cast<uint32_t>(a.Hkv), static_cast<uint32_t>(a.max_parts),
                              static_cast<uint32_t>(rows));
-  const size_t lds = static_cast<size_t>(decode_lds_floats(W, a.G, D) * 4);
-  hipLaunchKernelGGL((attn_decode_kernel<TT, D, W>), grid, dim3(64 * W), lds, stream, a);
+  AttnArgs da = a;
+  da.dec_slots = decode_slots(W, a.G, D);
+  const size_t lds = static_cast<size_t>(decode_lds_words(W, da.dec_slots, a.G, D) * 4);
+  hipLaunchKernelGGL((attn_decode_kernel<TT, D, W>), grid, dim3(64 * W), lds, stream, da);
 }
 
 template <class TT, int D>
 static void launch_mfma(const AttnArgs& a, int waves, int64_t rows, int64_t max_q, int64_t n_dec,
-                        int64_t n_pre, hipStream_t stream) {
+                        int64_t n_pre, int64_t n_merge, hipStream_t stream) {
   if (!a.sched || n_dec > 0) {
-    if (waves == 16)
-      launch_decode<TT, D, 16>(a, rows, n_dec, stream);
-    else
+    if constexpr (D <= 128) {
+      if (waves == 16)
+        launch_decode<TT, D, 16>(a, rows, n_dec, stream);
+      else
+        launch_decode<TT, D, 8>(a, rows, n_dec, stream);
+    } else {
       launch_decode<TT, D, 8>(a, rows, n_dec, stream);
-    if (a.max_parts > 1) {
-      dim3 mgrid(static_cast<uint32_t>((a.Hq * (D / 8) + 255) / 256),
-                 static_cast<uint32_t>(rows));
-      hipLaunchKernelGGL((attn_merge_kernel<TT, D>), mgrid, dim3(256), 0, stream, a);
+    }
+    if (a.sched ? n_merge > 0 : a.max_parts > 1) {
+      dim3 mgrid = a.sched ? dim3(static_cast<uint32_t>(n_merge))
+                           : dim3(static_cast<uint32_t>((a.Hq * (D / 8) + 63) / 64), static_cast<uint32_t>(rows));
+      hipLaunchKernelGGL((attn_merge_kernel<TT, D>), mgrid, dim3(64), 0, stream, a);
     }
   }
   if (a.sched ? n_pre > 0 : max_q >= 2) {
@@ -999,7 +1202,7 @@ extern "C" int64_t kvhot_paged_attention_workspace_bytes(
     return KVHOT_EINVAL;
   const Plan pl = make_plan(num_rows, max_q_len, max_k_len, num_q_heads, num_kv_heads,
                             head_dim, block_size, partition_tokens, dtype);
-  return pl.workspace_bytes();
+  return pl.grid_ok ? pl.workspace_bytes(num_q_heads / num_kv_heads, head_dim) : 0;
 }
 
 extern "C" int64_t kvhot_paged_attention_schedule(
@@ -1008,12 +1211,14 @@ extern "C" int64_t kvhot_paged_attention_schedule(
     int64_t num_rows, int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim,
     int64_t block_size, int64_t partition_tokens, int is_causal, int dtype,
     int32_t* units, int64_t capacity_units, int64_t* num_decode_units,
-    int64_t* num_prefill_units, int64_t* partition_tokens_used) {
+    int64_t* num_prefill_units, int64_t* num_merge_units, int64_t* workspace_bytes) {
   clear_error();
   if (num_rows < 0 || num_q_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0 ||
       block_size <= 0 || partition_tokens < 0 || num_q_heads % num_kv_heads != 0 ||
       dtype_size(dtype) == 0 || capacity_units < 0 || bt_row_stride < 0)
     return set_error(KVHOT_EINVAL, "paged_attention_schedule: bad sizes");
+  if (num_rows > 65535 || num_q_heads > 65535)
+    return set_error(KVHOT_EUNSUPPORTED, "paged_attention_schedule: rows or heads too large");
   if (num_rows > 0 && (!q_lens || !k_lens || !q_starts || !q_pos_offsets ||
                        (bt_row_stride > 0 && !block_table)))
     return set_error(KVHOT_EINVAL, "paged_attention_schedule: null host arrays");
@@ -1026,38 +1231,40 @@ extern "C" int64_t kvhot_paged_attention_schedule(
     max_q = std::max<int64_t>(max_q, q_lens[r]);
     max_k = std::max<int64_t>(max_k, k_lens[r]);
   }
-  std::vector<int4> dec, pre;
+  std::vector<int4> dec, pre, mrg;
+  int64_t partials = 0;
   const Plan pl = make_plan(num_rows, max_q, max_k, num_q_heads, num_kv_heads, head_dim,
                             block_size, partition_tokens, dtype);
-  int64_t pt_used = partition_tokens;
   if (pl.mfma) {
     const int64_t G = num_q_heads / num_kv_heads;
-    const int64_t resident = resident_decode_waves(dtype, head_dim, pl.waves, G);
-    pt_used = plan_decode(q_lens, k_lens, q_pos_offsets, q_starts, block_table, bt_row_stride,
-                          block_size, num_rows, num_kv_heads, is_causal != 0, pl.waves, resident,
-                          partition_tokens, dec);
-    plan_prefill(q_lens, k_lens, q_pos_offsets, num_rows, num_kv_heads, G, head_dim,
-                 is_causal != 0, pre);
-    const Plan check = make_plan(num_rows, max_q, max_k, num_q_heads, num_kv_heads, head_dim,
-                                 block_size, pt_used, dtype);
-    if (!check.mfma) {  // too many partitions for the grid: no schedule
+    const int64_t groups = resident_decode_waves(dtype, head_dim, pl.waves, G) / pl.waves;
+    if (plan_decode(q_lens, k_lens, q_pos_offsets, q_starts, block_table, bt_row_stride, block_size,
+                    num_rows, num_kv_heads, is_causal != 0, pl.waves, groups, partition_tokens, dec,
+                    mrg, partials)) {
+      plan_prefill(q_lens, k_lens, q_pos_offsets, num_rows, num_kv_heads, G, head_dim,
+                   is_causal != 0, pre);
+    } else {  // counts beyond the descriptor fields: no schedule
       dec.clear();
-      pre.clear();
-      pt_used = partition_tokens;
+      mrg.clear();
+      partials = 0;
     }
   }
-  if (partition_tokens_used) *partition_tokens_used = pt_used;
-  // Units are 8 int32 (two int4) each: decode waves, then prefill work-groups.
+  // Units are 8 int32 (two int4) each: decode waves, prefill work-groups,
+  // merge units.
   const int64_t n_dec = static_cast<int64_t>(dec.size() / 2);
   const int64_t n_pre = static_cast<int64_t>(pre.size() / 2);
+  const int64_t n_mrg = static_cast<int64_t>(mrg.size() / 2);
   if (num_decode_units) *num_decode_units = n_dec;
   if (num_prefill_units) *num_prefill_units = n_pre;
-  if (units && capacity_units >= n_dec + n_pre) {
+  if (num_merge_units) *num_merge_units = n_mrg;
+  if (workspace_bytes) *workspace_bytes = partials * partial_bytes(num_q_heads / num_kv_heads, head_dim);
+  if (units && capacity_units >= n_dec + n_pre + n_mrg) {
     int4* out = reinterpret_cast<int4*>(units);
     std::copy(dec.begin(), dec.end(), out);
     std::copy(pre.begin(), pre.end(), out + dec.size());
+    std::copy(mrg.begin(), mrg.end(), out + dec.size() + pre.size());
   }
-  return n_dec + n_pre;
+  return n_dec + n_pre + n_mrg;
 }
 
 extern "C" int kvhot_paged_attention(
@@ -1071,14 +1278,14 @@ extern "C" int kvhot_paged_attention(
     int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim,
     int64_t block_size, int64_t num_blocks, float scale, int is_causal,
     int dtype, int64_t partition_tokens, const int32_t* schedule,
-    int64_t num_decode_units, int64_t num_prefill_units, void* workspace,
-    int64_t workspace_bytes, void* stream) {
+    int64_t num_decode_units, int64_t num_prefill_units, int64_t num_merge_units,
+    void* workspace, int64_t workspace_bytes, void* stream) {
   clear_error();
   const int64_t es = dtype_size(dtype);
   if (es == 0) return set_error(KVHOT_EINVAL, "paged_attention: bad dtype");
   if (num_rows < 0 || total_query < 0 || max_q_len < 0 || max_k_len < 0 ||
       num_q_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0 || block_size <= 0 ||
-      num_blocks < 0 || bt_row_stride < 0 || partition_tokens < 0)
+      num_blocks < 0 || bt_row_stride < 0 || partition_tokens < 0 || workspace_bytes < 0)
     return set_error(KVHOT_EINVAL, "paged_attention: bad sizes");
   if (num_q_heads % num_kv_heads != 0)
     return set_error(KVHOT_EINVAL, "paged_attention: num_q_heads % num_kv_heads != 0");
@@ -1121,14 +1328,18 @@ extern "C" int kvhot_paged_attention(
   a.total_q = total_query;
   const int64_t n_dec = schedule ? num_decode_units : 0;
   const int64_t n_pre = schedule ? num_prefill_units : 0;
-  if (schedule && (n_dec < 0 || n_pre < 0 || n_dec > 0x7fffffff || n_pre > 0x7fffffff))
+  const int64_t n_mrg = schedule ? num_merge_units : 0;
+  if (schedule && (n_dec < 0 || n_pre < 0 || n_mrg < 0 || n_dec > 0x7fffffff ||
+                   n_pre > 0x7fffffff || n_mrg > 0x7fffffff))
     return set_error(KVHOT_EINVAL, "paged_attention: bad schedule unit counts");
   a.sched = reinterpret_cast<const int4*>(schedule);
+  a.merge_units = (schedule && n_mrg > 0) ? a.sched + 2 * (n_dec + n_pre) : nullptr;
   a.max_parts = 1;
   hipStream_t s = static_cast<hipStream_t>(stream);
 
   Plan pl = make_plan(num_rows, max_q_len, max_k_len, num_q_heads, num_kv_heads, head_dim,
                       block_size, partition_tokens, dtype);
+  if (!schedule && !pl.grid_ok) pl.mfma = false;
   if (schedule && pl.mfma && n_dec % pl.waves != 0)
     return set_error(KVHOT_EINVAL, "paged_attention: decode schedule is not whole work-groups");
   if (pl.mfma) {
@@ -1143,18 +1354,21 @@ extern "C" int kvhot_paged_attention(
     if (!aligned) pl.mfma = false;
   }
   if (pl.mfma) {
-    if (pl.max_parts > 1) {
-      if (!workspace || workspace_bytes < pl.workspace_bytes())
+    const int64_t pb = partial_bytes(a.G, head_dim);
+    const int64_t need = schedule ? (n_mrg > 0 ? pb : 0) : pl.workspace_bytes(a.G, head_dim);
+    if (need > 0) {
+      if (!workspace || workspace_bytes < need)
         return set_error(KVHOT_EWORKSPACE,
-                         "paged_attention: workspace of " + std::to_string(pl.workspace_bytes()) +
-                             " bytes required");
-      char* ws = static_cast<char*>(workspace);
-      a.ws_lse = reinterpret_cast<float*>(ws);
-      a.ws_o = reinterpret_cast<float*>(ws + pl.lse_bytes);
+                         "paged_attention: workspace of " + std::to_string(need) + " bytes required");
+      a.num_partials = schedule ? workspace_bytes / pb : pl.partials;
+      a.ws_o = static_cast<float*>(workspace);
+      a.ws_lse = a.ws_o + a.num_partials * a.G * head_dim;
     }
-    a.part_tokens = pl.part_tokens;
-    a.max_parts = pl.max_parts;
-#define KVHOT_MFMA(TT, DD) launch_mfma<TT, DD>(a, pl.waves, num_rows, max_q_len, n_dec, n_pre, s)
+    if (!schedule) {
+      a.part_tokens = pl.part_tokens;
+      a.max_parts = pl.max_parts;
+    }
+#define KVHOT_MFMA(TT, DD) launch_mfma<TT, DD>(a, pl.waves, num_rows, max_q_len, n_dec, n_pre, n_mrg, s)
     if (dtype == KVHOT_BF16) {
       if (head_dim == 64) KVHOT_MFMA(BF16, 64);
       else if (head_dim == 128) KVHOT_MFMA(BF16, 128);

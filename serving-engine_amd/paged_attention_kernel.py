@@ -57,39 +57,38 @@ def _workspace(device: torch.device, stream: int, nbytes: int) -> torch.Tensor |
 
 
 def _schedule(metadata, device, hq, hkv, d, bs, pt, causal, dtype):
-    """(device units, n_decode, n_prefill, partition_tokens) of
+    """(device units, n_decode, n_prefill, n_merge, workspace bytes) of
     kvhot_paged_attention_schedule for this step, built once per attention
-    shape from the host length copies and cached in the metadata dict;
-    (None, 0, 0, pt) without host copies."""
+    shape from the host copies of the metadata and cached in the metadata
+    dict; None without host copies."""
     host_q = metadata.get("host_q_lens")
     if host_q is None:
-        return None, 0, 0, pt
+        return None
     key = (hq, hkv, d, bs, pt, bool(causal), dtype, str(device))
     cache = metadata.setdefault("_schedules", {})
-    hit = cache.get(key)
-    if hit is not None:
-        return hit
+    if key in cache:
+        return cache[key]
     host_k = metadata["host_k_lens"]
     host_off = metadata["host_q_pos_offsets"]
     host_qs = metadata["host_q_starts"]
     host_bt = metadata["host_block_table"]
     lib = _lib.load()
-    n_dec, n_pre, pt_used = ctypes.c_int64(0), ctypes.c_int64(0), ctypes.c_int64(pt)
+    counts = [ctypes.c_int64(0) for _ in range(4)]  # decode, prefill, merge units; workspace bytes
     args = (host_q.ctypes.data, host_k.ctypes.data, host_qs.ctypes.data, host_off.ctypes.data,
             host_bt.ctypes.data if host_bt.size else None, host_bt.shape[1] if host_bt.ndim == 2 else 0,
             len(host_q), hq, hkv, d, bs, pt, 1 if causal else 0, dtype)
-    outs = (ctypes.byref(n_dec), ctypes.byref(n_pre), ctypes.byref(pt_used))
+    outs = tuple(ctypes.byref(c) for c in counts)
     total = lib.kvhot_paged_attention_schedule(*args, None, 0, *outs)
     if total < 0:
         _lib.check(int(total), "kvhot_paged_attention_schedule")
     if total == 0:
-        hit = (None, 0, 0, pt)
+        hit = None
     else:
         units = torch.empty((total, 8), dtype=torch.int32, pin_memory=True)
         got = lib.kvhot_paged_attention_schedule(*args, units.data_ptr(), total, *outs)
         if got != total:
             _lib.check(-1 if got >= 0 else int(got), "kvhot_paged_attention_schedule")
-        hit = (units.to(device, non_blocking=True), n_dec.value, n_pre.value, int(pt_used.value))
+        hit = (units.to(device, non_blocking=True),) + tuple(int(c.value) for c in counts)
     cache[key] = hit
     return hit
 
@@ -122,8 +121,8 @@ def paged_flash_attention(q, k_cache, v_cache, metadata, num_q_heads, num_kv_hea
     head_dim], one layer of the block pool; metadata: the dict of
     build_paged_batch_metadata().  Returns ``o`` shaped and strided like q
     (``torch.empty_like(q)``) and ``l`` = natural-log LSE, fp32
-    [total_query, num_q_heads].  ``partition_tokens`` (extension) fixes the
-    split-K partition size of decode rows.
+    [total_query, num_q_heads].  ``partition_tokens`` (extension) cuts
+    decode rows into split-K partitions of at most that many keys.
     """
     if q.dim() != 3 or k_cache.dim() != 4 or v_cache.dim() != 4:
         raise ValueError("expected q [T, Hq, D] and k_cache/v_cache [N, block_size, Hkv, D]")
@@ -161,13 +160,17 @@ def paged_flash_attention(q, k_cache, v_cache, metadata, num_q_heads, num_kv_hea
 
     lib = _lib.load()
     stream = _lib.stream_handle(device)
-    sched, n_dec, n_pre, pt = _schedule(metadata, device, num_q_heads, num_kv_heads, head_dim,
-                                        block_size, pt, is_causal, dtype)
-    need = lib.kvhot_paged_attention_workspace_bytes(
-        num_rows, total_query, max_q, max_k, num_q_heads, num_kv_heads, head_dim,
-        block_size, pt, dtype)
-    if need < 0:
-        _lib.check(int(need), "kvhot_paged_attention_workspace_bytes")
+    plan = _schedule(metadata, device, num_q_heads, num_kv_heads, head_dim, block_size, pt,
+                     is_causal, dtype)
+    if plan is not None:
+        sched, n_dec, n_pre, n_mrg, need = plan
+    else:
+        sched, n_dec, n_pre, n_mrg = None, 0, 0, 0
+        need = lib.kvhot_paged_attention_workspace_bytes(
+            num_rows, total_query, max_q, max_k, num_q_heads, num_kv_heads, head_dim,
+            block_size, pt, dtype)
+        if need < 0:
+            _lib.check(int(need), "kvhot_paged_attention_workspace_bytes")
     ws = _workspace(device, stream, need)
     status = lib.kvhot_paged_attention(
         q.data_ptr(), _lib.i64_array(q.stride()),
@@ -180,7 +183,7 @@ def paged_flash_attention(q, k_cache, v_cache, metadata, num_q_heads, num_kv_hea
         metadata["q_starts"].data_ptr(), metadata["q_pos_offsets"].data_ptr(),
         num_rows, total_query, max_q, max_k, num_q_heads, num_kv_heads, head_dim,
         block_size, num_blocks, float(scale), 1 if is_causal else 0, dtype, pt,
-        sched.data_ptr() if sched is not None else None, n_dec, n_pre,
+        sched.data_ptr() if sched is not None else None, n_dec, n_pre, n_mrg,
         ws.data_ptr() if ws is not None else None, ws.numel() if ws is not None else 0,
         stream)
     _lib.check(status, "kvhot_paged_attention")

@@ -73,7 +73,7 @@ def test_attention_rejects_bad_arguments(lib):
     q3, c4, l2 = _i64(4096, 128, 1), _i64(16384, 1024, 128, 1), _i64(32, 1)
     f = FAKE
     args = [f, q3, f, c4, f, c4, f, q3, f, l2, f, 8, f, f, f, f,
-            4, 4, 1, 100, 32, 8, 128, 16, 64, 0.1, 1, 2, 64, None, 0, 0, None, 0, None]
+            4, 4, 1, 100, 32, 8, 128, 16, 64, 0.1, 1, 2, 64, None, 0, 0, 0, None, 0, None]
     bad = list(args)
     bad[20] = 30  # Hq not a multiple of Hkv
     assert lib.kvhot_paged_attention(*bad) == -1
@@ -98,9 +98,9 @@ def test_attention_rejects_bad_arguments(lib):
 
 def test_workspace_bytes(lib):
     # decode: 64 rows, max ctx 2048, 32/8 heads, D=128, 256-token partitions
-    # -> LSE 64*32*8*4 B, partials 64*32*8*128*4 B
+    # -> 64 rows x 8 kv heads x 8 parts partials of 4 heads x (128 + 1) floats
     n = lib.kvhot_paged_attention_workspace_bytes(64, 64, 1, 2048, 32, 8, 128, 16, 256, 2)
-    assert n == 65536 + 64 * 32 * 8 * 128 * 4
+    assert n == 64 * 8 * 8 * 4 * (128 + 1) * 4
     # one partition: no workspace
     assert lib.kvhot_paged_attention_workspace_bytes(4, 4, 1, 130, 12, 12, 64, 16, 512, 2) == 0
     # fp32 runs the VALU kernel, which never splits
@@ -109,6 +109,8 @@ def test_workspace_bytes(lib):
 
 
 def _schedule(lib, q_lens, k_lens, offs, hq=32, hkv=8, d=128, pt=0, causal=1, dtype=2):
+    """Runs the host planner; returns (decode descriptors as dicts, prefill
+    units, merge units, workspace bytes, query token of each row)."""
     import numpy as np
 
     q = np.asarray(q_lens, np.int32)
@@ -117,65 +119,91 @@ def _schedule(lib, q_lens, k_lens, offs, hq=32, hkv=8, d=128, pt=0, causal=1, dt
     qs = np.concatenate([[0], np.cumsum(q)[:-1]]).astype(np.int32)
     mb = max(-(-int(x) // 16) for x in k)
     bt = (np.arange(len(q) * mb, dtype=np.int32).reshape(len(q), mb) + 1000)  # block ids 1000 + r*mb + j
-    nd, npf, ptu = ctypes.c_int64(), ctypes.c_int64(), ctypes.c_int64()
-    outs = (ctypes.byref(nd), ctypes.byref(npf), ctypes.byref(ptu))
+    cnt = [ctypes.c_int64() for _ in range(4)]
+    outs = tuple(ctypes.byref(c) for c in cnt)
     head = (q.ctypes.data, k.ctypes.data, qs.ctypes.data, o.ctypes.data, bt.ctypes.data, mb, len(q), hq, hkv,
             d, 16, pt, causal, dtype)
     total = lib.kvhot_paged_attention_schedule(*head, None, 0, *outs)
     units = np.zeros((max(total, 0), 8), np.int32)
     got = lib.kvhot_paged_attention_schedule(*head, units.ctypes.data, total, *outs)
     assert got == total
-    # decode descriptors carry (query token, visible keys, first block, query position)
-    for row, kvh, s0, s1, qtok, kend, first, qpos in units[:nd.value].tolist():
-        if row >= 0:
-            assert qtok == qs[row] and qpos == o[row] and kend == min(k[row], o[row] + 1)
-            assert first == 1000 + row * mb + (16 * s0) // 16
-    return units[:, :4], nd.value, npf.value, ptu.value
+    nd, npf, nm, ws = (c.value for c in cnt)
+    assert nd + npf + nm == total
+    dec = []
+    for x, y, s0, s1, qtok, kend, first, pidx in units[:nd].tolist():
+        if x < 0:
+            dec.append(None)
+            continue
+        row, nparts, kvh, part = x & 0xFFFF, x >> 16, y & 0xFFFF, y >> 16
+        # each descriptor carries its row's query token, visible keys and first block
+        assert qtok == qs[row] and kend == min(k[row], o[row] + 1)
+        assert first == (1000 + row * mb + s0 if s0 < s1 else -1)
+        dec.append(dict(row=row, nparts=nparts, kvh=kvh, part=part, s0=s0, s1=s1, pidx=pidx))
+    return dec, units[nd:nd + npf], units[nd + npf:], ws, qs
 
 
-def _check_decode_schedule(dec, waves_per_group, rows, hkv, pt, max_slices):
-    """Every (row, kv head, partition) of every decode row is covered exactly
-    once by contiguous waves of one work-group; no wave walks more than
-    max_slices slices."""
-    assert len(dec) % waves_per_group == 0
-    cover = {}
-    for g0 in range(0, len(dec), waves_per_group):
-        grp = dec[g0:g0 + waves_per_group]
-        seen_keys = set()
-        prev = None
-        for row, kvh, s0, s1 in grp.tolist():
-            if row < 0:
+def _check_decode_schedule(dec, merge, ws, qs, W, rows, hkv, G=4, D=128, pt=0):
+    """Every (row, kv head) key range of every decode row is covered exactly
+    once by parts; each part is one contiguous run of waves of one
+    work-group; split ranges have one merge unit whose partial indices are
+    theirs alone; the workspace holds every partial.  Returns the slices per
+    work-group."""
+    assert len(dec) % W == 0
+    cover, owner, loads = {}, {}, []
+    for g0 in range(0, len(dec), W):
+        grp = dec[g0:g0 + W]
+        load, prev = 0, None
+        for wv in grp:
+            if wv is None:
                 prev = None
                 continue
-            assert s1 - s0 <= max_slices
-            key = (row, kvh, (16 * s0) // pt)
+            key = (wv["row"], wv["kvh"], wv["part"])
             if key != prev:
-                assert key not in seen_keys, "segment split inside a work-group"
-                seen_keys.add(key)
+                assert key not in owner, "part in two places"
+                owner[key] = g0
             prev = key
-            cover.setdefault(key, []).append((s0, s1))
+            load += wv["s1"] - wv["s0"]
+            cover.setdefault((wv["row"], wv["kvh"]), []).append(wv)
+        loads.append(load)
+    base_of = {}
+    for qtok, kvh, nparts, base, *rest in merge.tolist():
+        assert rest == [0, 0, 0, 0]
+        base_of[(qtok, kvh)] = (nparts, base)
+    used = set()
     for row, kend in rows.items():
-        nparts = max(-(-kend // pt), 1)
-        for p in range(nparts):
-            kb, ke = p * pt, min(kend, (p + 1) * pt)
-            for h in range(hkv):
-                pieces = sorted(cover.pop((row, h, p)))
-                assert pieces[0][0] == kb // 16 and pieces[-1][1] == kb // 16 + -(-(ke - kb) // 16)
-                assert all(a[1] == b[0] for a, b in zip(pieces, pieces[1:]))
-    assert not cover
+        n = -(-kend // 16)
+        for h in range(hkv):
+            waves = sorted(cover.pop((row, h)), key=lambda w: (w["s0"], w["s1"]))
+            nparts = waves[0]["nparts"]
+            assert all(w["nparts"] == nparts for w in waves)
+            assert waves[0]["s0"] == 0 and waves[-1]["s1"] == n
+            assert all(a["s1"] == b["s0"] for a, b in zip(waves, waves[1:]))
+            parts = sorted({w["part"] for w in waves})
+            assert parts == list(range(nparts))
+            for w in waves:
+                if pt:
+                    assert w["part"] * pt // 16 <= w["s0"] and w["s1"] <= (w["part"] + 1) * pt // 16
+                if nparts > 1:
+                    used.add(w["pidx"])
+            if nparts > 1:
+                nm, base = base_of.pop((int(qs[row]), h))
+                assert nm == nparts
+                assert {w["pidx"] for w in waves} == set(range(base, base + nparts))
+                assert all(w["pidx"] == base + w["part"] for w in waves)
+    assert not cover and not base_of
+    assert ws == len(used) * G * (D + 1) * 4
+    return loads
 
 
 def test_schedule_lists_every_unit_once(lib):
-    """Host planner: decode waves cover every (row, kv head, partition) once,
-    balanced; prefill units every (row, kv head, query block); longest first."""
+    """Host planner: decode waves cover every (row, kv head, partition) once;
+    prefill units every (row, kv head, query block); longest first."""
     # rows: decode 300 keys, decode 40 keys, prefill 20 queries on 50 keys, empty chunk, decode 2000 keys
     q_lens, k_lens, offs = [1, 1, 20, 0, 1], [300, 40, 50, 16, 2000], [299, 39, 30, 16, 1999]
-    units, nd, npf, ptu = _schedule(lib, q_lens, k_lens, offs, pt=1024)
-    assert ptu == 1024
-    dec, pre = units[:nd], units[nd:]
-    assert len(pre) == npf
-    # 1024-key partitions over 16-wave groups: at most 1024 / 16 / 16 = 4 slices per wave
-    _check_decode_schedule(dec, 16, {0: 300, 1: 40, 4: 2000}, 8, 1024, 4)
+    dec, pre, merge, ws, qs = _schedule(lib, q_lens, k_lens, offs, pt=1024)
+    _check_decode_schedule(dec, merge, ws, qs, 16, {0: 300, 1: 40, 4: 2000}, 8, pt=1024)
+    # the 2000-key row has two 1024-key partitions per kv head, the others one
+    assert sorted(merge[:, 2].tolist()) == [2] * 8
     # prefill: 20 queries, 16 per block (64 m-rows / G=4) -> 2 blocks x 8 kv heads; the empty chunk has none
     assert sorted(map(tuple, pre[:, :3].tolist())) == sorted((2, h, b) for h in range(8) for b in range(2))
     # the second block (queries 16..19 at positions 46..49) sees 50 keys, the first 46
@@ -183,19 +211,38 @@ def test_schedule_lists_every_unit_once(lib):
     assert list(pre[:, 3]) == sorted(pre[:, 3], reverse=True)
 
 
-def test_schedule_chooses_partition_for_whole_batch(lib):
-    """Without a partition size the planner keeps every row in one partition
-    when the batch fits, with at least 8 slices per wave."""
+def test_schedule_balances_work_groups(lib):
+    """Without a partition size the planner gives every work-group of one
+    device-full (256 work-groups of 16 waves when no device is queried) the
+    same number of slices, splitting ranges only where a cut falls."""
     import numpy as np
 
     rng = np.random.default_rng(0)
     ctx = rng.integers(128, 2048, size=64, endpoint=True)
-    units, nd, npf, ptu = _schedule(lib, [1] * 64, ctx, ctx - 1)
-    assert npf == 0 and ptu >= 2048 and ptu % 256 == 0
-    _check_decode_schedule(units[:nd], 16, dict(enumerate(ctx.tolist())), 8, ptu, ptu // 256)
+    dec, pre, merge, ws, qs = _schedule(lib, [1] * 64, ctx, ctx - 1)
+    assert len(pre) == 0
+    loads = _check_decode_schedule(dec, merge, ws, qs, 16, dict(enumerate(ctx.tolist())), 8)
+    total = sum(-(-int(c) // 16) for c in ctx) * 8
+    target = -(-total // 256)
+    assert len(loads) <= 257
+    assert max(loads) <= target + max(2, target // 32)
+    # every cut leaves at least 4 slices on either side
+    assert len(merge) < len(loads)
+
+
+def test_schedule_tiny_rows_and_empty_rows(lib):
+    """Rows with no visible key still get a wave (it writes zeros); many tiny
+    rows are packed at most 16 ranges per work-group, unsplit."""
+    q_lens = [1] * 40
+    k_lens = [0, 5] + [17] * 38
+    offs = [0, 4] + [16] * 38
+    dec, pre, merge, ws, qs = _schedule(lib, q_lens, k_lens, offs, hq=8, hkv=8, d=64)
+    _check_decode_schedule(dec, merge, ws, qs, 16, dict(enumerate(min(k, o + 1) for k, o in zip(k_lens, offs))),
+                           8, G=1, D=64)
+    assert len(merge) == 0 and ws == 0
 
 
 def test_schedule_empty_for_vector_path(lib):
     # fp32 runs the VALU kernel: no launch list
-    units, nd, npf, _ = _schedule(lib, [1, 1], [100, 50], [99, 49], dtype=0)
-    assert len(units) == 0 and nd == 0 and npf == 0
+    dec, pre, merge, ws, _ = _schedule(lib, [1, 1], [100, 50], [99, 49], dtype=0)
+    assert len(dec) == 0 and len(pre) == 0 and len(merge) == 0 and ws == 0

@@ -217,10 +217,25 @@ def test_config2_decode(cuda, sea, wl, config2):
     T.kv_cache.copy_(snap)
     o, l = hip_step(sea, wl, w, T)
     assert_attention(w, o, l, ref_o, ref_l)
-    # same step again: the split-K counters left the workspace clean
+    # same step again: the workspace needs no clearing between calls.  Waves
+    # share out slices at run time, so the summation order (and only the last
+    # bits) may differ: within 2 bf16 ulps of the first run.
     T.kv_cache.copy_(snap)
     o2, l2 = hip_step(sea, wl, w, T)
-    assert torch.equal(o, o2) and torch.equal(l, l2)
+    torch.testing.assert_close(o2.float(), o.float(), atol=1e-3, rtol=2 ** -7)
+    torch.testing.assert_close(l2, l, atol=1e-5, rtol=1e-5)
+
+
+@pytest.mark.parametrize("pt", [None, 256])
+def test_config2_without_schedule(cuda, sea, wl, config2, pt):
+    """The padded-grid launch a caller gets without host length copies (no
+    schedule): device metadata only."""
+    w, T, snap, (ref_o, ref_l) = config2
+    announce(f"attention workload 2 without a schedule, partition {pt}")
+    T.kv_cache.copy_(snap)
+    meta = {k: v for k, v in wl.metadata_tensors(w, T.q.device).items() if not k.startswith("host_")}
+    o, l = hip_step(sea, wl, w, T, partition_tokens=pt, meta=meta)
+    assert_attention(w, o, l, ref_o, ref_l)
 
 
 def test_config2_matches_eager_restatement(cuda, sea, wl, config2):
@@ -264,13 +279,17 @@ def test_config4_prefix_sharing_and_cow(cuda, sea, wl):
     cache = sea._PagedKVCache(T.kv_cache)
     cache.copy_blocks(w.copy_src, w.copy_dst)
     meta = wl.metadata_tensors(w, cuda)
-    bt = meta["block_table"]
+    bt, host_bt = meta["block_table"], meta["host_block_table"]  # the schedule reads the host copy
     for i, x in enumerate(w.rows):
         bt[i, math.ceil(x.k_len / 16) - 1] = int(w.copy_dst[i])
+        host_bt[i, math.ceil(x.k_len / 16) - 1] = int(w.copy_dst[i])
+    assert torch.equal(bt.cpu(), torch.from_numpy(host_bt))
     kc, vc = cache.blocks(0)
     o2, l2 = sea.paged_flash_attention(T.q, kc, vc, meta, 32, 8, 1.0 / math.sqrt(128))
     torch.cuda.synchronize()
-    assert torch.equal(o, o2) and torch.equal(l, l2)
+    assert_attention(w, o2, l2, ref_o, ref_l)
+    torch.testing.assert_close(o2.float(), o.float(), atol=1e-3, rtol=2 ** -7)
+    torch.testing.assert_close(l2, l, atol=1e-5, rtol=1e-5)
 
 
 def test_config5_long_context_40gb_pool(cuda, sea, wl):
