@@ -10,13 +10,19 @@ workload (64 rows, ctx U[128, 2048], 32/8 heads, D=128, bf16, block 16, pool
 
 value = algorithmic bytes moved per step (K/V read + Q in + O out + block
 table + LSE out, plus the append's K/V read+write and slots) / step time, in
-GB/s (1e9).  roofline = the attention kernel alone: the same algorithmic bytes
-of one launch over its average duration, timed with HIP events on the launch
-stream across a run of back-to-back launches.  cpu_baseline = the reference's
-eager PyTorch path (restated in oracle/eager.py) on this host's cores, on one
-layer of the same batch.
+GB/s (1e9).  roofline = one attention call alone (the decode launch plus the
+merge launch for rows split across work-groups): its algorithmic bytes over
+its average duration, timed with HIP events on the launch stream across a run
+of back-to-back calls; `traffic` = the HBM bytes rocprofv3's FETCH_SIZE and
+WRITE_SIZE counters read for the same call, scaled by what they read for a
+copy of known size, as recorded in profiles/attention_decode_gqa64_traffic.md
+(null when that file is absent).  cpu_baseline = the reference's eager
+PyTorch path (restated in oracle/eager.py) on this host's cores, on one layer
+of the same batch.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload 2]
+       python bench.py --copy-probe   # kvhot_copy_blocks of 256 MiB each way
+                                      # (counter calibration)
 """
 from __future__ import annotations
 
@@ -33,6 +39,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "attention_decode_gqa64_traffic.md")
 
 
 def parse():
@@ -46,7 +53,40 @@ def parse():
     ap.add_argument("--kernel-reps", type=int, default=10, help="passes over all layers for the kernel timing")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=20.0, help="budget for the CPU baseline sample")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="only run kvhot_copy_blocks over 256 MiB each way, 5 times (counter calibration)")
     return ap.parse_args()
+
+
+def recorded_traffic(workload: int):
+    """HBM bytes per attention call recorded from the rocprofv3 counter runs
+    (a `traffic_bytes_per_call: N` line of TRAFFIC_FILE), for workload 2."""
+    if workload != 2 or not os.path.exists(TRAFFIC_FILE):
+        return None
+    with open(TRAFFIC_FILE) as f:
+        for line in f:
+            if line.strip().startswith("traffic_bytes_per_call:"):
+                return int(line.split(":", 1)[1].strip())
+    return None
+
+
+def copy_probe():
+    """kvhot_copy_blocks of 4096 block pairs (K and V, 32 KiB each): 256 MiB
+    read and 256 MiB written per launch, the known-size copy the counter
+    readings are scaled by."""
+    import torch
+
+    sea = importlib.import_module("serving-engine_amd")
+    dev = torch.device("cuda:0")
+    kv = torch.zeros((1, 2, 8192, 16, 8, 128), dtype=torch.bfloat16, device=dev)
+    cache = sea._PagedKVCache(kv)
+    src = torch.arange(0, 4096, dtype=torch.int64)
+    dst = torch.arange(4096, 8192, dtype=torch.int64)
+    for _ in range(5):
+        cache.copy_blocks(src, dst)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_probe": "kvhot_copy_blocks", "pairs": 4096, "read_bytes": 2 * 4096 * 32768,
+                      "write_bytes": 2 * 4096 * 32768, "launches": 5}), flush=True)
 
 
 def main():
@@ -55,6 +95,10 @@ def main():
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); this build has no "
               "multi-GPU path", file=sys.stderr)
         sys.exit(2)
+
+    if args.copy_probe:
+        copy_probe()
+        return
 
     import torch
 
@@ -153,12 +197,13 @@ def main():
         "pct_of_hbm_peak": round(100.0 * value / HBM_PEAK_GBS, 2),
         "roofline": {
             "bound": "hbm",
-            "kernel": "attn_mfma_kernel (split-K decode, fused partition merge)",
+            "kernel": "one attention call: attn_decode_kernel<BF16,128,16> + attn_merge_kernel<BF16,128> "
+                      "(rows split across work-groups)",
             "achieved": round(attn_gbs, 2),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(attn_gbs / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": recorded_traffic(args.workload),
             "algorithmic_bytes_per_launch": attn_bytes,
             "avg_launch_us": round(attn_us, 3),
         },
