@@ -40,6 +40,10 @@ def common_flags(defines: list[str]) -> list[str]:
         "-fPIC",
         # Packed FP32 (v_pk_*_f32) stays off: plain fp32 math only.
         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+        # MFMA accumulators in arch VGPRs: the prefill kernel rescales its
+        # output accumulators with VALU ops, which cannot read AGPRs.  (The
+        # decode and merge kernels compile to the same code either way.)
+        "-mllvm", "-amdgpu-mfma-vgpr-form=1",
         "-Wall",
         "-Wno-unused-command-line-argument",
     ]

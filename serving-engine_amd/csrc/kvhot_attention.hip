@@ -24,14 +24,17 @@
 //    which on gfx950 is an L2 write-back per wave -- far slower than a launch;
 //    partial stores interleaved with the K/V stream also cost bandwidth, so
 //    they are kept to long rows.)
-//  * attn_prefill_kernel<T, D, NM>: rows with q_len >= 2.  One wave per
-//    (row, kv head, block of 16*NM/G queries); causal mask from q_pos_offset;
-//    key tiles past the block's last query are never loaded.
+//  * attn_prefill_kernel<T, D, NM>: rows with q_len >= 2.  A work-group of 4
+//    waves per (row, kv head, 4 blocks of 16*NM/G queries) stages 32-key K/V
+//    tiles through LDS and shares them; both products use the 16x16x32 MFMA
+//    (P^T keeps S^T's key order as the K dimension).  Causal mask from
+//    q_pos_offset; tiles past the work-group's last query are never loaded.
 //  * attn_generic_kernel<T>: VALU kernel for fp32 (exact fp32 arithmetic) and
 //    for shapes the MFMA kernels do not cover.
 #include "kvhot_internal.h"
 
 #include <algorithm>
+#include <cfloat>
 #include <climits>
 #include <vector>
 
@@ -134,8 +137,24 @@ __device__ inline int decode_visible_keys(const AttnArgs& a, int row) {
                               static_cast<int64_t>(a.max_parts) * a.part_tokens));
 }
 
+// Prefill tiles move their softmax reference only when a score exceeds it by
+// more than this many log2 units (P < 2^kLazyRescale: with up to 2^31 keys and
+// |V| < 2^70 the fp32 sums stay finite).
+constexpr float kLazyRescale = 16.f;
+enum { kTileFast = 0, kTileFull = 1, kTileMasked = 2 };
+
+// max(a, b, c) as one v_max3_f32.  (fmaxf on MFMA results first quiets
+// possible signalling NaNs with an extra v_max per operand; scores that are
+// NaN give NaN rows either way.)
+__device__ inline float max3_raw(float a, float b, float c) {
+  float r;
+  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
+
+
 // One wavefront's attention state and key loop.
-template <class TT, int D, int NM, bool DB>
+template <class TT, int D, int NM>
 struct WaveAttn {
   static constexpr int NC = D / 32;
   static constexpr int EPL = D / 16;  // head_dim values per lane per V row; PV MFMAs per tile
@@ -267,47 +286,127 @@ struct WaveAttn {
     }
   }
 
-  // Online-softmax attention of every m-row over keys [kbeg, kstop) of `row`
-  // (kbeg a multiple of 16), walked in order.
-  __device__ void attend(const AttnArgs& a, int row, int kvh, int kbeg, int kstop, int qpos_min) {
-    const int lane = 16 * g + n;
-    const int bs = a.bs;
-    const int32_t* btrow = a.bt + static_cast<int64_t>(row) * a.bt_stride;
-    const int nb_row = min(static_cast<int64_t>((kstop + bs - 1) / bs), a.bt_stride);
-    // Windows of 64 blocks: lane j holds the id of logical block win + j,
-    // loaded once before the window's slices are walked.
-    for (int wbeg = kbeg; wbeg < kstop; wbeg += 64 * bs) {
-      const int wend = min(kstop, wbeg + 64 * bs);
-      const int win = wbeg / bs;
-      const int bt_reg = (win + lane < nb_row) ? btrow[win + lane] : 0;
-      auto block_of = [&](int ts) -> int64_t {
-        int64_t id = __builtin_amdgcn_readlane(bt_reg, ts / bs - win);
-        return id < 0 ? 0 : (id >= a.num_blocks ? a.num_blocks - 1 : id);
-      };
-      if constexpr (!DB) {
-        for (int ts = wbeg; ts < wend; ts += 16) {
-          KVSlice<D> T;
-          load_slice(a, kvh, block_of(ts), ts % bs, T);
-          compute_slice(a, ts, kstop, qpos_min, T);
-        }
-      } else {
-        KVSlice<D> A, B;
-        int ts = wbeg;
-        load_slice(a, kvh, block_of(ts), ts % bs, A);
-        while (true) {
-          bool more = ts + 16 < wend;
-          if (more) load_slice(a, kvh, block_of(ts + 16), (ts + 16) % bs, B);
-          compute_slice(a, ts, kstop, qpos_min, A);
-          ts += 16;
-          if (!more) break;
-          more = ts + 16 < wend;
-          if (more) load_slice(a, kvh, block_of(ts + 16), (ts + 16) % bs, A);
-          compute_slice(a, ts, kstop, qpos_min, B);
-          ts += 16;
-          if (!more) break;
+  // Folds the 32 keys ts..ts+31 of an LDS tile (PreTile layout, rows of
+  // Tile::RB bytes) into the
+  // online softmax, with v_mfma_f32_16x16x32 for both products.  The 32 keys
+  // are the K dimension of O^T += V^T . P^T in the order lane group g holds
+  // them in S^T -- keys 4g..4g+3 of the first 16, then 4g..4g+3 of the
+  // second -- so P^T is the B operand as it stands; V^T is gathered in that
+  // same key order.
+  //
+  // m[s] is a reference, not the exact running max: P = 2^(x - m) with x the
+  // score in log2 units, and m only moves when some score exceeds it by more
+  // than kLazyRescale, so P stays below 2^kLazyRescale.  While no lane sees
+  // such a score (the usual case once a row's first keys are in) a tile needs
+  // no cross-lane reduction and no rescale of O.  m starts at -FLT_MAX, so
+  // masked scores (-inf) give P = 0 and the first visible score takes the
+  // slow path.  sl = scale * log2(e) > 0 (a negative scale is folded into Q).
+  //
+  // MODE kTileFast: a tile with no masked key; returns false, with the state
+  // untouched, when some reference would have to move.  kTileFull and
+  // kTileMasked always fold the tile in.
+  template <class Tile, int MODE>
+  __device__ bool tile_lds(float sl, const char* kt, const char* vt, int ts, int kstop) {
+    f32x4 sc[NM][2];
+#pragma unroll
+    for (int s = 0; s < NM; ++s) sc[s][0] = sc[s][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+    // K row 16h + n, head_dim 8(4c+g) ..: one lane base plus constant offsets.
+    const char* kl = kt + n * Tile::RB + 16 * g;
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        const u32x4 kop = *reinterpret_cast<const u32x4*>(kl + 16 * h * Tile::RB + 64 * c);
+#pragma unroll
+        for (int s = 0; s < NM; ++s) sc[s][h] = TT::mfma(kop, qf[s][c], sc[s][h]);
+      }
+    if constexpr (MODE == kTileMasked) {
+#pragma unroll
+      for (int s = 0; s < NM; ++s)
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const int tk = ts + 16 * h + 4 * g + j;
+            sc[s][h][j] = (tk < kstop && tk <= qpos[s]) ? sc[s][h][j] : -INFINITY;
+          }
+    }
+    // V rows 4g+j and 16+4g+j, head_dim values EPL*n .. EPL*n + EPL - 1,
+    // read before the softmax so their latency is hidden behind it.
+    const char* vl = vt + 4 * g * Tile::RB + 2 * EPL * n;
+    constexpr int VC = VW < 4 ? 1 : VW / 4;  // 16-byte chunks of V per row and lane
+    constexpr int VD = VW < 4 ? VW : 4;      // dwords per chunk
+    uint32_t vr[8][VD];
+    auto read_v = [&](int c) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const char* p = vl + ((j & 3) + (j < 4 ? 0 : 16)) * Tile::RB + 16 * c;
+        if constexpr (VD == 2) {
+          const u32x2 v = *reinterpret_cast<const u32x2*>(p);
+          vr[j][0] = v.x; vr[j][1] = v.y;
+        } else {
+          const u32x4 v = *reinterpret_cast<const u32x4*>(p);
+          vr[j][0] = v.x; vr[j][1] = v.y; vr[j][2] = v.z; vr[j][3] = v.w;
         }
       }
+    };
+    read_v(0);
+    float mloc[NM];
+    bool need = false;
+#pragma unroll
+    for (int s = 0; s < NM; ++s) {
+      const float a = max3_raw(sc[s][0][0], sc[s][0][1], sc[s][0][2]);
+      const float b = max3_raw(sc[s][0][3], sc[s][1][0], sc[s][1][1]);
+      mloc[s] = max3_raw(a, b, fmaxf(sc[s][1][2], sc[s][1][3])) * sl;
+      need = need || mloc[s] > m[s] + kLazyRescale;
     }
+    if constexpr (MODE == kTileFast) {
+      if (__builtin_amdgcn_ballot_w64(need) != 0) return false;
+    } else if (__builtin_amdgcn_ballot_w64(need) != 0) {
+      // Some row has a score above its reference: move every row's reference
+      // to its exact running max and rescale.
+#pragma unroll
+      for (int s = 0; s < NM; ++s) {
+        float mx = fmaxf(mloc[s], __shfl_xor(mloc[s], 16, kWave));
+        mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+        const float mnew = fmaxf(m[s], mx);
+        const float corr = fast_exp2(m[s] - mnew);
+        m[s] = mnew;
+        l[s] *= corr;
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) o[s][e] *= corr;
+      }
+    }
+    u32x4 pb[NM];
+#pragma unroll
+    for (int s = 0; s < NM; ++s) {
+      float p[2][4];
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) p[h][j] = fast_exp2(__builtin_fmaf(sc[s][h][j], sl, -m[s]));
+      l[s] += ((p[0][0] + p[0][1]) + (p[0][2] + p[0][3])) + ((p[1][0] + p[1][1]) + (p[1][2] + p[1][3]));
+      pb[s] = u32x4{TT::pack2(p[0][0], p[0][1]), TT::pack2(p[0][2], p[0][3]),
+                    TT::pack2(p[1][0], p[1][1]), TT::pack2(p[1][2], p[1][3])};
+    }
+    // O^T += V^T . P^T, one 16-byte chunk of each V row at a time.
+#pragma unroll
+    for (int c = 0; c < VC; ++c) {
+      if (c > 0) read_v(c);
+#pragma unroll
+      for (int e2 = 0; e2 < 2 * VD; ++e2) {
+        const int e = 2 * VD * c + e2;
+        const int w = e2 >> 1;
+        const uint32_t sel = (e2 & 1) ? 0x07060302u : 0x05040100u;
+        const u32x4 va = {__builtin_amdgcn_perm(vr[1][w], vr[0][w], sel),
+                          __builtin_amdgcn_perm(vr[3][w], vr[2][w], sel),
+                          __builtin_amdgcn_perm(vr[5][w], vr[4][w], sel),
+                          __builtin_amdgcn_perm(vr[7][w], vr[6][w], sel)};
+#pragma unroll
+        for (int s = 0; s < NM; ++s) o[s][e] = TT::mfma(va, pb[s], o[s][e]);
+      }
+    }
+    return true;
   }
 
   // Row sums over the four lane groups that share an m-row.
@@ -490,7 +589,7 @@ attn_decode_kernel(const AttnArgs a) {
   // query position passed to the m-row setup is kend - 1.
   int krow = valid ? row : -1, kkvh = kvh, kpart = part, kkend = kend;
 
-  WaveAttn<TT, D, 1, false> wa;
+  WaveAttn<TT, D, 1> wa;
   wa.setup(a, lane, valid ? kvh : 0, qs, 0, valid ? 1 : 0, kend - 1);
   KVSlice<D> T;
   int i = s0;              // slice whose loads are in flight, if `have`
@@ -743,11 +842,43 @@ attn_merge_kernel(const AttnArgs a) {
 }
 
 // -------------------------------------------------------------- prefill --
-// One wave per (row, kv head, query block of 16*NM/G queries), no key split.
+// A work-group of kPreWaves waves takes consecutive query blocks of one
+// (row, kv head): wave w the 16*NM/G queries q0 + w*16*NM/G ... (all G heads of
+// each).  Keys are walked in 32-key tiles that the whole work-group stages
+// from the paged cache into LDS (double-buffered: tile t+1 is loaded into
+// registers while tile t is computed, then written to the other buffer), so
+// each K/V byte is read from HBM once per work-group and from LDS once per
+// wave.  A wave skips tiles wholly past its own causal limit.
+constexpr int kPreWaves = 8;  // two per SIMD
+constexpr int kPreKeys = 32;
+
+// A K (or V) tile in LDS: 32 key rows of RB bytes, head_dim contiguous plus
+// 16 bytes of padding.  With rows 4 banks apart, the MFMA operand reads --
+// 16 rows at one 16-byte chunk for K, one row at 16 consecutive chunks for V
+// -- fall in distinct banks, and every lane's reads are one base address plus
+// constant offsets.
+template <int D>
+struct PreTile {
+  static constexpr int CPR = D / 8;                     // 16-byte chunks per key row
+  static constexpr int RB = 2 * D + 16;                 // bytes per key row
+  static constexpr int BYTES = kPreKeys * RB;           // bytes per tile
+  static constexpr int CHUNKS = kPreKeys * CPR;         // chunks per tile
+  // 16-byte chunks each thread stages per tile (K and V each); with fewer
+  // chunks than threads only the first CHUNKS threads stage.
+  static constexpr int PER_THREAD = CHUNKS < 64 * kPreWaves ? 1 : CHUNKS / (64 * kPreWaves);
+  __device__ static inline int offset(int r, int ch) { return r * RB + 16 * ch; }
+};
+
 template <class TT, int D, int NM>
-__global__ void __launch_bounds__(64)
+__global__ void __launch_bounds__(64 * kPreWaves)
 attn_prefill_kernel(const AttnArgs a) {
-  const int lane = threadIdx.x;
+  using Tile = PreTile<D>;
+  using st = uint16_t;
+  constexpr int PT = Tile::PER_THREAD;
+  __shared__ __attribute__((aligned(16))) char smem[4 * Tile::BYTES];  // K0 V0 K1 V1
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
   int row, kvh, qblk;
   if (a.sched) {
     const int4 u = a.sched[2 * static_cast<int64_t>(blockIdx.x)];
@@ -759,20 +890,153 @@ attn_prefill_kernel(const AttnArgs a) {
     kvh = blockIdx.x % a.Hkv;
     qblk = blockIdx.x / a.Hkv;
   }
+  row = __builtin_amdgcn_readfirstlane(row);
+  kvh = __builtin_amdgcn_readfirstlane(kvh);
+  qblk = __builtin_amdgcn_readfirstlane(qblk);
+  if (row < 0 || kvh < 0 || kvh >= a.Hkv || qblk < 0) return;
   const int qlen = a.q_lens[row];
   if (qlen < 2) return;
-  const int QPW = 16 * NM / a.G;
-  const int q0 = qblk * QPW;
-  if (q0 >= qlen) return;
-  const int nq = min(QPW, qlen - q0);
+  const int QPW = 16 * NM / a.G;  // queries per wave
+  const int q0g = qblk * QPW * kPreWaves;
+  if (q0g >= qlen) return;
+  const int nqg = min(QPW * kPreWaves, qlen - q0g);
   const int off = a.q_offs[row];
   const int klen = a.k_lens[row];
-  const int kend = max(a.causal ? min(klen, off + q0 + nq) : klen, 0);
+  const int kend_g = max(a.causal ? min(klen, off + q0g + nqg) : klen, 0);
   const int64_t qs = a.q_starts[row];
+  // This wave's queries and the keys they see.
+  const int q0 = q0g + wave * QPW;
+  const int nq = max(min(QPW, nqg - wave * QPW), 0);
+  const int kend = nq > 0 ? max(a.causal ? min(klen, off + q0 + nq) : klen, 0) : 0;
+  const int qpos_min = a.causal ? off + q0 : INT_MAX;
 
-  WaveAttn<TT, D, NM, false> wa;
+  WaveAttn<TT, D, NM> wa;
   wa.setup(a, lane, kvh, qs, q0, nq, off);
-  if (kend > 0) wa.attend(a, row, kvh, 0, kend, a.causal ? off + q0 : INT_MAX);
+  // Scores in log2 units are S * sl with sl > 0: a negative scale flips the
+  // sign of Q (exact), a zero scale becomes a negligible positive one.
+  float sl = a.scale_log2;
+  if (sl < 0.f) {
+#pragma unroll
+    for (int s = 0; s < NM; ++s)
+#pragma unroll
+      for (int c = 0; c < WaveAttn<TT, D, NM>::NC; ++c) wa.qf[s][c] ^= u32x4{0x80008000u, 0x80008000u, 0x80008000u, 0x80008000u};
+    sl = -sl;
+  }
+  sl = fmaxf(sl, 1e-30f);
+#pragma unroll
+  for (int s = 0; s < NM; ++s) wa.m[s] = -FLT_MAX;
+
+  // Thread tid stages chunks tid + 256 i of each tile: key row r of the tile
+  // (in its 16-key half hf[i], the same for a whole wave), chunk ch.
+  int koff[PT], voff[PT], ldsc[PT], hrow[PT], hf[PT];
+#pragma unroll
+  for (int i = 0; i < PT; ++i) {
+    const int cid = tid + 64 * kPreWaves * i;
+    const int r = cid / Tile::CPR, ch = cid % Tile::CPR;
+    hrow[i] = r & 15;
+    hf[i] = __builtin_amdgcn_readfirstlane((64 * wave + 64 * kPreWaves * i) / (16 * Tile::CPR));
+    koff[i] = 2 * (hrow[i] * static_cast<int>(a.k_st) + 8 * ch);
+    voff[i] = 2 * (hrow[i] * static_cast<int>(a.v_st) + 8 * ch);
+    ldsc[i] = Tile::offset(r, ch);
+  }
+  const int bs = a.bs;
+  const int32_t* btrow = a.bt + static_cast<int64_t>(row) * a.bt_stride;
+  const int nb_row = static_cast<int>(min(static_cast<int64_t>((kend_g + bs - 1) / bs), a.bt_stride));
+  const st* kbase = static_cast<const st*>(a.k) + static_cast<int64_t>(kvh) * a.k_sh;
+  const st* vbase = static_cast<const st*>(a.v) + static_cast<int64_t>(kvh) * a.v_sh;
+  // Block ids of logical blocks win .. win + 63, one per lane; the 16-key
+  // slice to be staged next is at offset cur_bo of logical block cur_blk.
+  int win = 0;
+  int bt_reg = lane < nb_row ? btrow[lane] : 0;
+  int cur_blk = 0, cur_bo = 0;
+  u32x4 stk[PT], stv[PT];
+  const bool stager = tid < Tile::CHUNKS;  // whole waves
+
+  // Loads tile t (the next in order) into stk / stv; keys past kend_g are zero.
+  auto issue = [&](int t) {
+    if (!stager) return;
+    int64_t id[2];
+    int bo[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      if (cur_blk - win >= 64) {
+        win = cur_blk;
+        bt_reg = win + lane < nb_row ? btrow[win + lane] : 0;
+      }
+      int64_t b = __builtin_amdgcn_readlane(bt_reg, cur_blk - win);
+      id[h] = b < 0 ? 0 : (b >= a.num_blocks ? a.num_blocks - 1 : b);
+      bo[h] = cur_bo;
+      cur_bo += 16;
+      if (cur_bo >= bs) {
+        cur_bo = 0;
+        ++cur_blk;
+      }
+    }
+    const bool tail = kPreKeys * t + kPreKeys > kend_g;
+#pragma unroll
+    for (int i = 0; i < PT; ++i) {
+      const int h = hf[i];
+      const int64_t b = h ? id[1] : id[0];
+      const int o = h ? bo[1] : bo[0];
+      const __amdgpu_buffer_rsrc_t kr = block_rsrc(kbase + b * a.k_sb, static_cast<int>(2 * a.k_sb));
+      const __amdgpu_buffer_rsrc_t vr = block_rsrc(vbase + b * a.v_sb, static_cast<int>(2 * a.v_sb));
+      stk[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(kr, koff[i], 2 * o * static_cast<int>(a.k_st), 0));
+      stv[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(vr, voff[i], 2 * o * static_cast<int>(a.v_st), 0));
+      if (tail && kPreKeys * t + 16 * h + hrow[i] >= kend_g) {
+        stk[i] = u32x4{0u, 0u, 0u, 0u};
+        stv[i] = u32x4{0u, 0u, 0u, 0u};
+      }
+    }
+  };
+  auto stage = [&](int buf) {
+    if (!stager) return;
+#pragma unroll
+    for (int i = 0; i < PT; ++i) {
+      *reinterpret_cast<u32x4*>(smem + 2 * buf * Tile::BYTES + ldsc[i]) = stk[i];
+      *reinterpret_cast<u32x4*>(smem + (2 * buf + 1) * Tile::BYTES + ldsc[i]) = stv[i];
+    }
+  };
+
+  // Every wave walks all ntiles tiles in step (staging tile t + 1, then one
+  // barrier per tile).  Tiles [0, nfull) have no key masked for this wave;
+  // they go through the fast path, each run of fast tiles being one loop with
+  // a single path for the accumulators.  A fast tile that would have to move
+  // a reference -- always the first -- and the masked or empty tiles past
+  // nfull take the general path one at a time.
+  const int ntiles = (kend_g + kPreKeys - 1) / kPreKeys;
+  const int nfull = (a.causal ? min(kend, qpos_min + 1) : kend) / kPreKeys;
+  auto finish = [&](int t) {
+    if (t + 1 < ntiles) stage((t & 1) ^ 1);
+    __syncthreads();
+  };
+  if (ntiles > 0) {
+    issue(0);
+    stage(0);
+  }
+  __syncthreads();
+  int t = 0;
+  while (t < ntiles) {
+    bool issued = false;
+    for (; t < nfull; ++t) {
+      if (t + 1 < ntiles) issue(t + 1);
+      const char* kt = smem + 2 * (t & 1) * Tile::BYTES;
+      if (!wa.template tile_lds<Tile, kTileFast>(sl, kt, kt + Tile::BYTES, kPreKeys * t, kend)) {
+        issued = true;
+        break;
+      }
+      finish(t);
+    }
+    if (t >= ntiles) break;
+    if (!issued && t + 1 < ntiles) issue(t + 1);
+    const int ts = kPreKeys * t;
+    const char* kt = smem + 2 * (t & 1) * Tile::BYTES;
+    if (t < nfull)
+      wa.template tile_lds<Tile, kTileFull>(sl, kt, kt + Tile::BYTES, ts, kend);
+    else if (ts < kend)
+      wa.template tile_lds<Tile, kTileMasked>(sl, kt, kt + Tile::BYTES, ts, kend);
+    finish(t);
+    ++t;
+  }
   float ltot[NM];
   wa.row_sums(ltot);
 #pragma unroll
@@ -938,7 +1202,9 @@ static Plan make_plan(int64_t rows, int64_t max_q, int64_t max_k, int64_t Hq,
   return pl;
 }
 
-constexpr int prefill_nm(int64_t D) { return D <= 128 ? 4 : 2; }
+// 16-row tiles of (query, head) pairs per prefill wave: O^T takes 64 VGPRs
+// and Q 32 at every head_dim, so two waves fit on a SIMD.
+constexpr int prefill_nm(int64_t D) { return D == 64 ? 4 : (D == 128 ? 2 : 1); }
 
 // Decode work-groups the current device holds at once, times their waves
 // (4096 when no device can be queried).
@@ -1126,13 +1392,13 @@ static void plan_prefill(const int32_t* q_lens, const int32_t* k_lens, const int
   for (int64_t r = 0; r < rows; ++r) {
     const int64_t qlen = q_lens[r], klen = k_lens[r], off = q_offs[r];
     if (qlen < 2) continue;
-    const int64_t qpw = 16 * prefill_nm(D) / G;
+    const int64_t qpw = kPreWaves * 16 * prefill_nm(D) / G;  // queries per work-group
     for (int64_t qb = 0; qb * qpw < qlen; ++qb) {
       const int64_t q0 = qb * qpw, nq = std::min(qpw, qlen - q0);
       const int64_t kend = std::max<int64_t>(causal ? std::min(klen, off + q0 + nq) : klen, 0);
       for (int64_t h = 0; h < Hkv; ++h)
         pre.push_back(int4{static_cast<int>(r), static_cast<int>(h), static_cast<int>(qb),
-                           static_cast<int>((kend + 15) / 16)});
+                           static_cast<int>((kend + kPreKeys - 1) / kPreKeys)});
     }
   }
   std::stable_sort(pre.begin(), pre.end(), [](const int4& x, const int4& y) { return x.w > y.w; });
@@ -1177,13 +1443,13 @@ static void launch_mfma(const AttnArgs& a, int waves, int64_t rows, int64_t max_
   }
   if (a.sched ? n_pre > 0 : max_q >= 2) {
     constexpr int NM = prefill_nm(D);
-    const int64_t qpw = 16 * NM / a.G;
+    const int64_t qpw = kPreWaves * 16 * NM / a.G;
     const int64_t nqb = (max_q + qpw - 1) / qpw;
     dim3 grid = a.sched ? dim3(static_cast<uint32_t>(n_pre))
                         : dim3(static_cast<uint32_t>(a.Hkv * nqb), 1u, static_cast<uint32_t>(rows));
     AttnArgs pa = a;
     if (a.sched) pa.sched = a.sched + 2 * n_dec;
-    hipLaunchKernelGGL((attn_prefill_kernel<TT, D, NM>), grid, dim3(64), 0, stream, pa);
+    hipLaunchKernelGGL((attn_prefill_kernel<TT, D, NM>), grid, dim3(64 * kPreWaves), 0, stream, pa);
   }
 }
 

@@ -204,10 +204,24 @@ def test_schedule_lists_every_unit_once(lib):
     _check_decode_schedule(dec, merge, ws, qs, 16, {0: 300, 1: 40, 4: 2000}, 8, pt=1024)
     # the 2000-key row has two 1024-key partitions per kv head, the others one
     assert sorted(merge[:, 2].tolist()) == [2] * 8
-    # prefill: 20 queries, 16 per block (64 m-rows / G=4) -> 2 blocks x 8 kv heads; the empty chunk has none
-    assert sorted(map(tuple, pre[:, :3].tolist())) == sorted((2, h, b) for h in range(8) for b in range(2))
-    # the second block (queries 16..19 at positions 46..49) sees 50 keys, the first 46
-    assert sorted(set(pre[:, 3].tolist())) == [3, 4]
+    # prefill: 20 queries, 64 per work-group (4 waves x 64 m-rows / G=4) -> 1 block x 8 kv heads;
+    # the empty chunk has none
+    assert sorted(map(tuple, pre[:, :3].tolist())) == sorted((2, h, 0) for h in range(8))
+    # the block's last query (position 49) sees 50 keys: two 32-key tiles
+    assert sorted(set(pre[:, 3].tolist())) == [2]
+    assert list(pre[:, 3]) == sorted(pre[:, 3], reverse=True)
+
+
+def test_schedule_prefill_blocks_longest_first(lib):
+    """Prefill work-groups take 64 queries (G=4) and are listed by key tiles, most first."""
+    # one 150-query chunk at positions 100..249 (250 keys), one 40-query chunk on 40 keys
+    dec, pre, merge, ws, qs = _schedule(lib, [150, 40], [250, 40], [100, 0])
+    assert len(dec) == 0 and len(merge) == 0
+    units = sorted(map(tuple, pre[:, :4].tolist()))
+    # row 0: blocks of queries 0-63, 64-127, 128-149 -> visible keys 164, 228, 250 -> 6, 8, 8 tiles
+    want = [(0, h, b, t) for h in range(8) for b, t in ((0, 6), (1, 8), (2, 8))]
+    want += [(1, h, 0, 2) for h in range(8)]
+    assert units == sorted(want)
     assert list(pre[:, 3]) == sorted(pre[:, 3], reverse=True)
 
 
