@@ -396,3 +396,37 @@ def test_hf_attention_adapter(cuda, sea, wl):
     torch.cuda.synchronize()
     assert weights is None and out.shape == (1, w.total_query, 32, 128)
     np.testing.assert_allclose(f32(out[0]), ref_o, **TOL[torch.bfloat16])
+
+
+@pytest.mark.parametrize("pattern,scale_sign", [("rising", 1.0), ("falling", 1.0), ("random", -1.0),
+                                                ("random", 0.0)])
+def test_prefill_softmax_reference_moves(cuda, sea, wl, pattern, scale_sign):
+    """Scores that climb by ~33 log2 units per 32-key tile (every tile moves
+    the softmax reference past the lazy threshold), scores that fall (later
+    probabilities underflow), and negative / zero scales."""
+    w = custom(wl, [(100, 400, 300), (1, 257, 256), (64, 64, 0), (40, 200, 160)], 32, 8, 128,
+               torch.bfloat16)
+    announce(f"prefill softmax reference: {pattern} scores, scale sign {scale_sign}")
+    T = wl.make_tensors(w, cuda)
+    if pattern != "random":
+        gen = torch.Generator(device=cuda)
+        gen.manual_seed(7)
+        u = torch.randn(128, generator=gen, device=cuda)
+        u = u / u.norm()
+        for row in w.rows:
+            j = torch.arange(row.k_len, device=cuda)
+            ramp = 2.0 * (j if pattern == "rising" else row.k_len - j).float()
+            blocks = torch.as_tensor(row.block_table, device=cuda)[j // 16]
+            kslice = T.kv_cache[0, 0, blocks, j % 16].float()  # [k_len, Hkv, D]
+            T.kv_cache[0, 0, blocks, j % 16] = (kslice + ramp[:, None, None] * u).to(T.kv_cache.dtype)
+        T.q.copy_((T.q.float() + 4.0 * u).to(T.q.dtype))
+    scale = scale_sign / math.sqrt(128)
+    kc, vc = sea._PagedKVCache(T.kv_cache).blocks(0)
+    o, l = sea.paged_flash_attention(T.q, kc, vc, wl.metadata_tensors(w, cuda), 32, 8, scale)
+    torch.cuda.synchronize()
+    q_lens, k_lens, q_starts, offs, bt = w.arrays()
+    ref_o, ref_l = paged_ref.paged_attention(f32(T.q), f32(T.kv_cache[0, 0]), f32(T.kv_cache[0, 1]),
+                                             q_lens, k_lens, q_starts, offs, bt, 32, 8, scale)
+    assert np.isfinite(f32(o)).all()
+    np.testing.assert_allclose(f32(o), ref_o, **TOL[torch.bfloat16])
+    np.testing.assert_allclose(l.cpu().numpy(), ref_l, atol=2e-3, rtol=2e-4)
