@@ -36,6 +36,7 @@
 #include <algorithm>
 #include <cfloat>
 #include <climits>
+#include <type_traits>
 #include <vector>
 
 namespace kvhot {
@@ -78,6 +79,16 @@ struct AttnArgs {
 };
 
 __device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+// 16 bytes per lane from r at byte offset off into LDS at dst + 16 * lane
+// (buffer_load_dwordx4 ... lds; offsets past the descriptor's range give
+// zeros).  A plain device function: the builtin needs a device target
+// feature, and inside a kernel template the host pass would drop the kernel.
+__device__ inline void dma16(__amdgpu_buffer_rsrc_t r, void* dst, int off) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr_t)dst, 16, off, 0, 0, 0);
+}
 
 // Buffer resource over [base, base + bytes): loads through it take a 32-bit
 // lane offset (no 64-bit per-lane address registers), and the hardware returns
@@ -141,16 +152,7 @@ __device__ inline int decode_visible_keys(const AttnArgs& a, int row) {
 // more than this many log2 units (P < 2^kLazyRescale: with up to 2^31 keys and
 // |V| < 2^70 the fp32 sums stay finite).
 constexpr float kLazyRescale = 16.f;
-enum { kTileFast = 0, kTileFull = 1, kTileMasked = 2 };
-
-// max(a, b, c) as one v_max3_f32.  (fmaxf on MFMA results first quiets
-// possible signalling NaNs with an extra v_max per operand; scores that are
-// NaN give NaN rows either way.)
-__device__ inline float max3_raw(float a, float b, float c) {
-  float r;
-  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
-  return r;
-}
+constexpr float kLazyLimit = 65536.f;  // 2^kLazyRescale
 
 
 // One wavefront's attention state and key loop.
@@ -286,98 +288,76 @@ struct WaveAttn {
     }
   }
 
-  // Folds the 32 keys ts..ts+31 of an LDS tile (PreTile layout, rows of
-  // Tile::RB bytes) into the
-  // online softmax, with v_mfma_f32_16x16x32 for both products.  The 32 keys
-  // are the K dimension of O^T += V^T . P^T in the order lane group g holds
-  // them in S^T -- keys 4g..4g+3 of the first 16, then 4g..4g+3 of the
-  // second -- so P^T is the B operand as it stands; V^T is gathered in that
-  // same key order.
+  // ---- 32-key LDS tiles (PreTile layout, rows of Tile::RB bytes) ----
+  // Both products use v_mfma_f32_16x16x32.  The 32 keys are the K dimension
+  // of O^T += V^T . P^T in the order lane group g holds them in S^T -- keys
+  // 4g..4g+3 of the first 16, then 4g..4g+3 of the second -- so P^T is the B
+  // operand as it stands; V^T is gathered in that same key order.
   //
   // m[s] is a reference, not the exact running max: P = 2^(x - m) with x the
   // score in log2 units, and m only moves when some score exceeds it by more
   // than kLazyRescale, so P stays below 2^kLazyRescale.  While no lane sees
   // such a score (the usual case once a row's first keys are in) a tile needs
   // no cross-lane reduction and no rescale of O.  m starts at -FLT_MAX, so
-  // masked scores (-inf) give P = 0 and the first visible score takes the
-  // slow path.  sl = scale * log2(e) > 0 (a negative scale is folded into Q).
-  //
-  // MODE kTileFast: a tile with no masked key; returns false, with the state
-  // untouched, when some reference would have to move.  kTileFull and
-  // kTileMasked always fold the tile in.
-  template <class Tile, int MODE>
-  __device__ bool tile_lds(float sl, const char* kt, const char* vt, int ts, int kstop) {
-    f32x4 sc[NM][2];
+  // masked scores (-inf) give P = 0 and the first visible score moves it.
+  // sl = scale * log2(e) > 0 (a negative scale is folded into Q).
+  static constexpr int VC = VW < 4 ? 1 : VW / 4;  // 16-byte chunks of V per row and lane
+  static constexpr int VD = VW < 4 ? VW : 4;      // dwords per chunk
+
+  // Raw S^T of a tile: lane (n, g) gets keys 4g+j (sc[s][0]) and 16+4g+j
+  // (sc[s][1]) of m-row n.
+  template <class Tile>
+  __device__ void qk_lds(const char* kt, f32x4 (&sc)[NM][2]) const {
 #pragma unroll
     for (int s = 0; s < NM; ++s) sc[s][0] = sc[s][1] = f32x4{0.f, 0.f, 0.f, 0.f};
-    // K row 16h + n, head_dim 8(4c+g) ..: one lane base plus constant offsets.
-    const char* kl = kt + n * Tile::RB + 16 * g;
+    // K row 16h + n, head_dim 8(4c+g) .. 8(4c+g)+7 (logical chunk 4c+g).
 #pragma unroll
     for (int h = 0; h < 2; ++h)
 #pragma unroll
       for (int c = 0; c < NC; ++c) {
-        const u32x4 kop = *reinterpret_cast<const u32x4*>(kl + 16 * h * Tile::RB + 64 * c);
+        const u32x4 kop = *reinterpret_cast<const u32x4*>(kt + Tile::offset(16 * h + n, 4 * c + g));
 #pragma unroll
         for (int s = 0; s < NM; ++s) sc[s][h] = TT::mfma(kop, qf[s][c], sc[s][h]);
       }
-    if constexpr (MODE == kTileMasked) {
+  }
+
+  // Chunk c of V rows 4g+j and 16+4g+j (j < 4), head_dim values from EPL*n.
+  template <class Tile>
+  __device__ void read_v(const char* vt, int c, uint32_t (&vr)[8][VD]) const {
 #pragma unroll
-      for (int s = 0; s < NM; ++s)
-#pragma unroll
-        for (int h = 0; h < 2; ++h)
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const int tk = ts + 16 * h + 4 * g + j;
-            sc[s][h][j] = (tk < kstop && tk <= qpos[s]) ? sc[s][h][j] : -INFINITY;
-          }
-    }
-    // V rows 4g+j and 16+4g+j, head_dim values EPL*n .. EPL*n + EPL - 1,
-    // read before the softmax so their latency is hidden behind it.
-    const char* vl = vt + 4 * g * Tile::RB + 2 * EPL * n;
-    constexpr int VC = VW < 4 ? 1 : VW / 4;  // 16-byte chunks of V per row and lane
-    constexpr int VD = VW < 4 ? VW : 4;      // dwords per chunk
-    uint32_t vr[8][VD];
-    auto read_v = [&](int c) {
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const char* p = vl + ((j & 3) + (j < 4 ? 0 : 16)) * Tile::RB + 16 * c;
-        if constexpr (VD == 2) {
-          const u32x2 v = *reinterpret_cast<const u32x2*>(p);
-          vr[j][0] = v.x; vr[j][1] = v.y;
-        } else {
-          const u32x4 v = *reinterpret_cast<const u32x4*>(p);
-          vr[j][0] = v.x; vr[j][1] = v.y; vr[j][2] = v.z; vr[j][3] = v.w;
-        }
+    for (int j = 0; j < 8; ++j) {
+      const int r = 4 * g + (j & 3) + (j < 4 ? 0 : 16);
+      const char* p = VD == 2 ? vt + Tile::offset(r, n >> 1) + 8 * (n & 1)
+                              : vt + Tile::offset(r, (VW / 4) * n + c);
+      if constexpr (VD == 2) {
+        const u32x2 v = *reinterpret_cast<const u32x2*>(p);
+        vr[j][0] = v.x; vr[j][1] = v.y;
+      } else {
+        const u32x4 v = *reinterpret_cast<const u32x4*>(p);
+        vr[j][0] = v.x; vr[j][1] = v.y; vr[j][2] = v.z; vr[j][3] = v.w;
       }
-    };
-    read_v(0);
-    float mloc[NM];
+    }
+  }
+
+  // Local (per-lane) max of each m-row's scores, in log2 units, and whether
+  // any exceeds its reference by more than kLazyRescale.
+  __device__ bool lazy_check(float sl, const f32x4 (&sc)[NM][2], float (&mloc)[NM]) const {
     bool need = false;
 #pragma unroll
     for (int s = 0; s < NM; ++s) {
-      const float a = max3_raw(sc[s][0][0], sc[s][0][1], sc[s][0][2]);
-      const float b = max3_raw(sc[s][0][3], sc[s][1][0], sc[s][1][1]);
-      mloc[s] = max3_raw(a, b, fmaxf(sc[s][1][2], sc[s][1][3])) * sl;
+      mloc[s] = fmaxf(fmaxf(fmaxf(sc[s][0][0], sc[s][0][1]), fmaxf(sc[s][0][2], sc[s][0][3])),
+                      fmaxf(fmaxf(sc[s][1][0], sc[s][1][1]), fmaxf(sc[s][1][2], sc[s][1][3]))) * sl;
       need = need || mloc[s] > m[s] + kLazyRescale;
     }
-    if constexpr (MODE == kTileFast) {
-      if (__builtin_amdgcn_ballot_w64(need) != 0) return false;
-    } else if (__builtin_amdgcn_ballot_w64(need) != 0) {
-      // Some row has a score above its reference: move every row's reference
-      // to its exact running max and rescale.
-#pragma unroll
-      for (int s = 0; s < NM; ++s) {
-        float mx = fmaxf(mloc[s], __shfl_xor(mloc[s], 16, kWave));
-        mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
-        const float mnew = fmaxf(m[s], mx);
-        const float corr = fast_exp2(m[s] - mnew);
-        m[s] = mnew;
-        l[s] *= corr;
-#pragma unroll
-        for (int e = 0; e < EPL; ++e) o[s][e] *= corr;
-      }
-    }
-    u32x4 pb[NM];
+    return need;
+  }
+
+  // P = 2^(S sl - m) as the packed B operand of the PV product, and this
+  // lane's row sums.  Returns whether some P exceeds 2^kLazyRescale (a score
+  // more than kLazyRescale above its reference, which the fast path may not
+  // take); the test reads P, so P is formed before any branch on it.
+  __device__ bool probs(float sl, const f32x4 (&sc)[NM][2], u32x4 (&pb)[NM], float (&lsum)[NM]) const {
+    bool big = false;
 #pragma unroll
     for (int s = 0; s < NM; ++s) {
       float p[2][4];
@@ -385,14 +365,22 @@ struct WaveAttn {
       for (int h = 0; h < 2; ++h)
 #pragma unroll
         for (int j = 0; j < 4; ++j) p[h][j] = fast_exp2(__builtin_fmaf(sc[s][h][j], sl, -m[s]));
-      l[s] += ((p[0][0] + p[0][1]) + (p[0][2] + p[0][3])) + ((p[1][0] + p[1][1]) + (p[1][2] + p[1][3]));
+      lsum[s] = ((p[0][0] + p[0][1]) + (p[0][2] + p[0][3])) + ((p[1][0] + p[1][1]) + (p[1][2] + p[1][3]));
+      const float pm = fmaxf(fmaxf(fmaxf(p[0][0], p[0][1]), fmaxf(p[0][2], p[0][3])),
+                             fmaxf(fmaxf(p[1][0], p[1][1]), fmaxf(p[1][2], p[1][3])));
+      big = big || !(pm <= kLazyLimit);
       pb[s] = u32x4{TT::pack2(p[0][0], p[0][1]), TT::pack2(p[0][2], p[0][3]),
                     TT::pack2(p[1][0], p[1][1]), TT::pack2(p[1][2], p[1][3])};
     }
-    // O^T += V^T . P^T, one 16-byte chunk of each V row at a time.
+    return big;
+  }
+
+  // O^T += V^T . P^T; vr holds chunk 0 of the V rows on entry.
+  template <class Tile>
+  __device__ void pv_lds(const char* vt, uint32_t (&vr)[8][VD], const u32x4 (&pb)[NM]) {
 #pragma unroll
     for (int c = 0; c < VC; ++c) {
-      if (c > 0) read_v(c);
+      if (c > 0) read_v<Tile>(vt, c, vr);
 #pragma unroll
       for (int e2 = 0; e2 < 2 * VD; ++e2) {
         const int e = 2 * VD * c + e2;
@@ -406,7 +394,66 @@ struct WaveAttn {
         for (int s = 0; s < NM; ++s) o[s][e] = TT::mfma(va, pb[s], o[s][e]);
       }
     }
+  }
+
+  // A tile with no masked key whose scores all stay within kLazyRescale of
+  // their references.  Returns false, with the state untouched, otherwise.
+  template <class Tile>
+  __device__ bool tile_fast(float sl, const char* kt, const char* vt) {
+    f32x4 sc[NM][2];
+    qk_lds<Tile>(kt, sc);
+    uint32_t vr[8][VD];
+    read_v<Tile>(vt, 0, vr);
+    u32x4 pb[NM];
+    float lsum[NM];
+    if (__builtin_amdgcn_ballot_w64(probs(sl, sc, pb, lsum)) != 0) return false;
+#pragma unroll
+    for (int s = 0; s < NM; ++s) l[s] += lsum[s];
+    pv_lds<Tile>(vt, vr, pb);
     return true;
+  }
+
+  // A whole tile with every step: keys at or past kstop or past an m-row's
+  // causal limit masked when MASK, references moved and O rescaled when a
+  // score calls for it.
+  template <class Tile, bool MASK>
+  __device__ void tile_general(float sl, const char* kt, const char* vt, int ts, int kstop) {
+    f32x4 sc[NM][2];
+    qk_lds<Tile>(kt, sc);
+    if constexpr (MASK) {
+#pragma unroll
+      for (int s = 0; s < NM; ++s)
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const int tk = ts + 16 * h + 4 * g + j;
+            sc[s][h][j] = (tk < kstop && tk <= qpos[s]) ? sc[s][h][j] : -INFINITY;
+          }
+    }
+    uint32_t vr[8][VD];
+    read_v<Tile>(vt, 0, vr);
+    float mloc[NM];
+    if (__builtin_amdgcn_ballot_w64(lazy_check(sl, sc, mloc)) != 0) {
+      // Move every row's reference to its exact running max and rescale.
+#pragma unroll
+      for (int s = 0; s < NM; ++s) {
+        float mx = fmaxf(mloc[s], __shfl_xor(mloc[s], 16, kWave));
+        mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+        const float mnew = fmaxf(m[s], mx);
+        const float corr = fast_exp2(m[s] - mnew);
+        m[s] = mnew;
+        l[s] *= corr;
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) o[s][e] *= corr;
+      }
+    }
+    u32x4 pb[NM];
+    float lsum[NM];
+    probs(sl, sc, pb, lsum);
+#pragma unroll
+    for (int s = 0; s < NM; ++s) l[s] += lsum[s];
+    pv_lds<Tile>(vt, vr, pb);
   }
 
   // Row sums over the four lane groups that share an m-row.
@@ -844,38 +891,76 @@ attn_merge_kernel(const AttnArgs a) {
 // -------------------------------------------------------------- prefill --
 // A work-group of kPreWaves waves takes consecutive query blocks of one
 // (row, kv head): wave w the 16*NM/G queries q0 + w*16*NM/G ... (all G heads of
-// each).  Keys are walked in 32-key tiles that the whole work-group stages
-// from the paged cache into LDS (double-buffered: tile t+1 is loaded into
-// registers while tile t is computed, then written to the other buffer), so
-// each K/V byte is read from HBM once per work-group and from LDS once per
+// each).  Keys are walked in 32-key tiles that the work-group copies from the
+// paged cache straight into LDS (buffer_load ... lds, no register staging)
+// through a ring of four slots, three tiles ahead of the one being computed,
+// so each K/V byte is read from HBM once per work-group and from LDS once per
 // wave.  A wave skips tiles wholly past its own causal limit.
 constexpr int kPreWaves = 8;  // two per SIMD
 constexpr int kPreKeys = 32;
+constexpr int kPreSlots = 4;
 
-// A K (or V) tile in LDS: 32 key rows of RB bytes, head_dim contiguous plus
-// 16 bytes of padding.  With rows 4 banks apart, the MFMA operand reads --
-// 16 rows at one 16-byte chunk for K, one row at 16 consecutive chunks for V
-// -- fall in distinct banks, and every lane's reads are one base address plus
-// constant offsets.
+// A K (or V) tile in LDS: 32 key rows of 2*D bytes.  The 16-byte chunks of a
+// row are XOR-swizzled (chunk lc of row r sits at lc ^ swz(r)), so the MFMA
+// operand reads -- 16 rows at one logical chunk for K, one row at 16
+// consecutive chunks for V -- fall in distinct banks of the 64.  A DMA
+// instruction fills 64 consecutive chunks (1 KiB); each lane picks the global
+// chunk that belongs at its position.
 template <int D>
 struct PreTile {
-  static constexpr int CPR = D / 8;                     // 16-byte chunks per key row
-  static constexpr int RB = 2 * D + 16;                 // bytes per key row
-  static constexpr int BYTES = kPreKeys * RB;           // bytes per tile
-  static constexpr int CHUNKS = kPreKeys * CPR;         // chunks per tile
-  // 16-byte chunks each thread stages per tile (K and V each); with fewer
-  // chunks than threads only the first CHUNKS threads stage.
-  static constexpr int PER_THREAD = CHUNKS < 64 * kPreWaves ? 1 : CHUNKS / (64 * kPreWaves);
-  __device__ static inline int offset(int r, int ch) { return r * RB + 16 * ch; }
+  static constexpr int CPR = D / 8;              // 16-byte chunks per key row
+  static constexpr int RB = 2 * D;               // bytes per key row
+  static constexpr int BYTES = kPreKeys * RB;    // bytes per K (or V) tile
+  static constexpr int CHUNKS = kPreKeys * CPR;  // chunks per tile
+  // Waves that issue the DMA of a tile, and DMA instructions each (K or V).
+  static constexpr int ISSUERS = CHUNKS / 64 < kPreWaves ? CHUNKS / 64 : kPreWaves;
+  static constexpr int NI = CHUNKS / (64 * ISSUERS);
+  // 128-byte rows (D = 64) share a 256-byte bank line in pairs.
+  __host__ __device__ static constexpr int swz(int r) { return D == 64 ? (r >> 1) & 7 : r & 15; }
+  __host__ __device__ static constexpr int offset(int r, int lc) { return r * RB + 16 * (lc ^ swz(r)); }
 };
+
+// s_waitcnt vmcnt(N) alone (expcnt and lgkmcnt at their no-wait maximum).
+template <int N>
+__device__ inline void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+// Work-group barrier for LDS filled by DMA: the caller has waited for its own
+// DMA (vmcnt); LDS reads are drained first so a slot can be refilled after.
+// The empty asm statements keep the compiler from moving memory accesses
+// across it (the s_barrier intrinsic alone does not order them).
+__device__ inline void lds_barrier() {
+  __builtin_amdgcn_s_waitcnt((15) | (7 << 4) | (0 << 8) | (3 << 14));  // lgkmcnt(0)
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
 
 template <class TT, int D, int NM>
 __global__ void __launch_bounds__(64 * kPreWaves)
 attn_prefill_kernel(const AttnArgs a) {
   using Tile = PreTile<D>;
+  using WA = WaveAttn<TT, D, NM>;
   using st = uint16_t;
-  constexpr int PT = Tile::PER_THREAD;
-  __shared__ __attribute__((aligned(16))) char smem[4 * Tile::BYTES];  // K0 V0 K1 V1
+  // Ring slots, K tile then V tile.  Separate arrays: the compiler can tell
+  // that reads of one slot do not alias the DMA into another, and so does
+  // not wait for every DMA in flight before each LDS read.
+  __shared__ __attribute__((aligned(16))) char slot0[2 * Tile::BYTES];
+  __shared__ __attribute__((aligned(16))) char slot1[2 * Tile::BYTES];
+  __shared__ __attribute__((aligned(16))) char slot2[2 * Tile::BYTES];
+  __shared__ __attribute__((aligned(16))) char slot3[2 * Tile::BYTES];
+  // Every call passes a constant slot, so after inlining each access names
+  // one array.
+  auto slot = [&](int S) -> char* {
+    switch (S) {
+      case 0: return slot0;
+      case 1: return slot1;
+      case 2: return slot2;
+      default: return slot3;
+    }
+  };
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63;
@@ -910,7 +995,7 @@ attn_prefill_kernel(const AttnArgs a) {
   const int kend = nq > 0 ? max(a.causal ? min(klen, off + q0 + nq) : klen, 0) : 0;
   const int qpos_min = a.causal ? off + q0 : INT_MAX;
 
-  WaveAttn<TT, D, NM> wa;
+  WA wa;
   wa.setup(a, lane, kvh, qs, q0, nq, off);
   // Scores in log2 units are S * sl with sl > 0: a negative scale flips the
   // sign of Q (exact), a zero scale becomes a negligible positive one.
@@ -919,123 +1004,146 @@ attn_prefill_kernel(const AttnArgs a) {
 #pragma unroll
     for (int s = 0; s < NM; ++s)
 #pragma unroll
-      for (int c = 0; c < WaveAttn<TT, D, NM>::NC; ++c) wa.qf[s][c] ^= u32x4{0x80008000u, 0x80008000u, 0x80008000u, 0x80008000u};
+      for (int c = 0; c < WA::NC; ++c) wa.qf[s][c] ^= u32x4{0x80008000u, 0x80008000u, 0x80008000u, 0x80008000u};
     sl = -sl;
   }
   sl = fmaxf(sl, 1e-30f);
 #pragma unroll
   for (int s = 0; s < NM; ++s) wa.m[s] = -FLT_MAX;
 
-  // Thread tid stages chunks tid + 256 i of each tile: key row r of the tile
-  // (in its 16-key half hf[i], the same for a whole wave), chunk ch.
-  int koff[PT], voff[PT], ldsc[PT], hrow[PT], hf[PT];
+  // DMA: issuing wave w, instruction i fills chunks 64 (NI w + i) .. of a
+  // tile; all of a wave's chunks lie in the one 16-key half hw.  Lane L's
+  // chunk is physical chunk pc of row pr; it loads logical chunk
+  // pc ^ swz(pr) of that key.
+  constexpr int NI = Tile::NI;
+  const bool issuer = wave < Tile::ISSUERS;
+  const int hw = __builtin_amdgcn_readfirstlane((64 * NI * wave) / (16 * Tile::CPR));
+  uint32_t koff[NI], voff[NI];
 #pragma unroll
-  for (int i = 0; i < PT; ++i) {
-    const int cid = tid + 64 * kPreWaves * i;
-    const int r = cid / Tile::CPR, ch = cid % Tile::CPR;
-    hrow[i] = r & 15;
-    hf[i] = __builtin_amdgcn_readfirstlane((64 * wave + 64 * kPreWaves * i) / (16 * Tile::CPR));
-    koff[i] = 2 * (hrow[i] * static_cast<int>(a.k_st) + 8 * ch);
-    voff[i] = 2 * (hrow[i] * static_cast<int>(a.v_st) + 8 * ch);
-    ldsc[i] = Tile::offset(r, ch);
+  for (int i = 0; i < NI; ++i) {
+    const int p = 64 * (NI * wave + i) + lane;
+    const int pr = p / Tile::CPR, pc = p % Tile::CPR;
+    const int lc = pc ^ Tile::swz(pr);
+    koff[i] = 2u * ((pr & 15) * static_cast<uint32_t>(a.k_st) + 8u * lc);
+    voff[i] = 2u * ((pr & 15) * static_cast<uint32_t>(a.v_st) + 8u * lc);
   }
   const int bs = a.bs;
   const int32_t* btrow = a.bt + static_cast<int64_t>(row) * a.bt_stride;
   const int nb_row = static_cast<int>(min(static_cast<int64_t>((kend_g + bs - 1) / bs), a.bt_stride));
-  const st* kbase = static_cast<const st*>(a.k) + static_cast<int64_t>(kvh) * a.k_sh;
-  const st* vbase = static_cast<const st*>(a.v) + static_cast<int64_t>(kvh) * a.v_sh;
-  // Block ids of logical blocks win .. win + 63, one per lane; the 16-key
-  // slice to be staged next is at offset cur_bo of logical block cur_blk.
-  int win = 0;
-  int bt_reg = lane < nb_row ? btrow[lane] : 0;
-  int cur_blk = 0, cur_bo = 0;
-  u32x4 stk[PT], stv[PT];
-  const bool stager = tid < Tile::CHUNKS;  // whole waves
+  const char* kbase = static_cast<const char*>(a.k) + 2 * static_cast<int64_t>(kvh) * a.k_sh;
+  const char* vbase = static_cast<const char*>(a.v) + 2 * static_cast<int64_t>(kvh) * a.v_sh;
+  // Byte strides; a block and the rows of a block fit 32 bits (checked on
+  // the host: block strides below 2^31 bytes).
+  const uint32_t ksb = 2u * static_cast<uint32_t>(a.k_sb), vsb = 2u * static_cast<uint32_t>(a.v_sb);
+  const uint32_t kst = 2u * static_cast<uint32_t>(a.k_st), vst = 2u * static_cast<uint32_t>(a.v_st);
+  const uint32_t nblocks = static_cast<uint32_t>(a.num_blocks);
+  // Block ids come through scalar loads (constant address space), fetched
+  // one tile ahead: nid is the physical block holding this wave's half of
+  // the next tile to load, at row nbo of logical block nblk.  (A vector load
+  // here would make the compiler wait for every DMA in flight before using
+  // it.)
+  const __attribute__((address_space(4))) int32_t* btc =
+      (const __attribute__((address_space(4))) int32_t*)btrow;
+  auto bt_at = [&](int blk) -> int { return btc[min(blk, max(nb_row - 1, 0))]; };
+  int nblk = (16 * hw) / bs, nbo = (16 * hw) % bs;
+  int nid = nb_row > 0 ? bt_at(nblk) : 0;
 
-  // Loads tile t (the next in order) into stk / stv; keys past kend_g are zero.
-  auto issue = [&](int t) {
-    if (!stager) return;
-    int64_t id[2];
-    int bo[2];
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      if (cur_blk - win >= 64) {
-        win = cur_blk;
-        bt_reg = win + lane < nb_row ? btrow[win + lane] : 0;
-      }
-      int64_t b = __builtin_amdgcn_readlane(bt_reg, cur_blk - win);
-      id[h] = b < 0 ? 0 : (b >= a.num_blocks ? a.num_blocks - 1 : b);
-      bo[h] = cur_bo;
-      cur_bo += 16;
-      if (cur_bo >= bs) {
-        cur_bo = 0;
-        ++cur_blk;
-      }
-    }
-    const bool tail = kPreKeys * t + kPreKeys > kend_g;
-#pragma unroll
-    for (int i = 0; i < PT; ++i) {
-      const int h = hf[i];
-      const int64_t b = h ? id[1] : id[0];
-      const int o = h ? bo[1] : bo[0];
-      const __amdgpu_buffer_rsrc_t kr = block_rsrc(kbase + b * a.k_sb, static_cast<int>(2 * a.k_sb));
-      const __amdgpu_buffer_rsrc_t vr = block_rsrc(vbase + b * a.v_sb, static_cast<int>(2 * a.v_sb));
-      stk[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(kr, koff[i], 2 * o * static_cast<int>(a.k_st), 0));
-      stv[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(vr, voff[i], 2 * o * static_cast<int>(a.v_st), 0));
-      if (tail && kPreKeys * t + 16 * h + hrow[i] >= kend_g) {
-        stk[i] = u32x4{0u, 0u, 0u, 0u};
-        stv[i] = u32x4{0u, 0u, 0u, 0u};
+  // DMA of tile t (the next in order) into ring slot S.  The descriptor of
+  // the half starts at its first key and covers only keys below kend_g: the
+  // rows past it read as zeros.
+  auto issue = [&](int S, int t) {
+    if (!issuer) return;
+    const uint32_t b = min(static_cast<uint32_t>(max(nid, 0)), nblocks - 1);
+    const int rows = min(max(kend_g - (kPreKeys * t + 16 * hw), 0), 16);
+    const char* kb = kbase + (static_cast<uint64_t>(b) * ksb + static_cast<uint32_t>(nbo) * kst);
+    const char* vb = vbase + (static_cast<uint64_t>(b) * vsb + static_cast<uint32_t>(nbo) * vst);
+    const int nrk = __builtin_amdgcn_readfirstlane(rows * static_cast<int>(kst));
+    const int nrv = __builtin_amdgcn_readfirstlane(rows * static_cast<int>(vst));
+    // This half of tile t + 1 (32 keys on), and its block id.
+    if (bs == 16) {
+      nblk += 2;
+    } else {
+      nbo += kPreKeys;
+      if (nbo >= bs) {
+        nbo -= bs;
+        ++nblk;
       }
     }
-  };
-  auto stage = [&](int buf) {
-    if (!stager) return;
+    nid = bt_at(nblk);
+    char* dst = slot(S) + 1024 * NI * wave;
 #pragma unroll
-    for (int i = 0; i < PT; ++i) {
-      *reinterpret_cast<u32x4*>(smem + 2 * buf * Tile::BYTES + ldsc[i]) = stk[i];
-      *reinterpret_cast<u32x4*>(smem + (2 * buf + 1) * Tile::BYTES + ldsc[i]) = stv[i];
+    for (int i = 0; i < NI; ++i) {
+      dma16(block_rsrc(kb, nrk), dst + 1024 * i, koff[i]);
+      dma16(block_rsrc(vb, nrv), dst + Tile::BYTES + 1024 * i, voff[i]);
     }
   };
 
-  // Every wave walks all ntiles tiles in step (staging tile t + 1, then one
-  // barrier per tile).  Tiles [0, nfull) have no key masked for this wave;
-  // they go through the fast path, each run of fast tiles being one loop with
-  // a single path for the accumulators.  A fast tile that would have to move
-  // a reference -- always the first -- and the masked or empty tiles past
-  // nfull take the general path one at a time.
+  // Every wave walks all ntiles tiles in step.  Tile t sits in slot t % 4;
+  // while it is computed, tiles t+1 and t+2 are landing and the DMA of tile
+  // t+3 is issued.  After tile t: wait until tile t+1 has landed (this wave's
+  // DMAs of tiles t+2 and t+3 may stay in flight), then one barrier.
+  constexpr int PER_TILE = 2 * NI;  // DMA instructions per issuing wave and tile
   const int ntiles = (kend_g + kPreKeys - 1) / kPreKeys;
-  const int nfull = (a.causal ? min(kend, qpos_min + 1) : kend) / kPreKeys;
   auto finish = [&](int t) {
-    if (t + 1 < ntiles) stage((t & 1) ^ 1);
-    __syncthreads();
+    if (t + 1 < ntiles) {
+      const int later = min(t + 3, ntiles - 1) - (t + 1);
+      if (later >= 2) wait_vmcnt<2 * PER_TILE>();
+      else if (later == 1) wait_vmcnt<PER_TILE>();
+      else wait_vmcnt<0>();
+    }
+    lds_barrier();
   };
-  if (ntiles > 0) {
-    issue(0);
-    stage(0);
-  }
-  __syncthreads();
+  if (ntiles > 0) issue(0, 0);
+  if (ntiles > 1) issue(1, 1);
+  if (ntiles > 2) issue(2, 2);
+  if (ntiles > 2) wait_vmcnt<2 * PER_TILE>();
+  else if (ntiles > 1) wait_vmcnt<PER_TILE>();
+  else wait_vmcnt<0>();
+  lds_barrier();
+
+  // Tiles [0, nfull) have no key masked for this wave.  Runs of four of them
+  // starting at slot 0 go through the fast path, one straight-line loop body
+  // per four tiles (a single path for the accumulators); a fast tile that
+  // would have to move a reference -- always the first -- and every other
+  // tile take the general path one at a time.
+  const int nfull = (a.causal ? min(kend, qpos_min + 1) : kend) / kPreKeys;
+  auto fast = [&](int S, int t) -> bool {
+    if (t + 3 < ntiles) issue((S + 3) % kPreSlots, t + 3);
+    const char* kt = slot(S);
+    return wa.template tile_fast<Tile>(sl, kt, kt + Tile::BYTES);
+  };
+  auto general = [&](int S, int t, bool issued) {
+    if (!issued && t + 3 < ntiles) issue((S + 3) % kPreSlots, t + 3);
+    const char* kt = slot(S);
+    const int ts = kPreKeys * t;
+    if (t < nfull)
+      wa.template tile_general<Tile, false>(sl, kt, kt + Tile::BYTES, ts, kend);
+    else if (ts < kend)
+      wa.template tile_general<Tile, true>(sl, kt, kt + Tile::BYTES, ts, kend);
+  };
   int t = 0;
   while (t < ntiles) {
     bool issued = false;
-    for (; t < nfull; ++t) {
-      if (t + 1 < ntiles) issue(t + 1);
-      const char* kt = smem + 2 * (t & 1) * Tile::BYTES;
-      if (!wa.template tile_lds<Tile, kTileFast>(sl, kt, kt + Tile::BYTES, kPreKeys * t, kend)) {
-        issued = true;
-        break;
+    if ((t & 3) == 0) {
+      while (t + 3 < nfull) {
+        if (!fast(0, t)) { issued = true; break; }
+        finish(t++);
+        if (!fast(1, t)) { issued = true; break; }
+        finish(t++);
+        if (!fast(2, t)) { issued = true; break; }
+        finish(t++);
+        if (!fast(3, t)) { issued = true; break; }
+        finish(t++);
       }
-      finish(t);
     }
     if (t >= ntiles) break;
-    if (!issued && t + 1 < ntiles) issue(t + 1);
-    const int ts = kPreKeys * t;
-    const char* kt = smem + 2 * (t & 1) * Tile::BYTES;
-    if (t < nfull)
-      wa.template tile_lds<Tile, kTileFull>(sl, kt, kt + Tile::BYTES, ts, kend);
-    else if (ts < kend)
-      wa.template tile_lds<Tile, kTileMasked>(sl, kt, kt + Tile::BYTES, ts, kend);
-    finish(t);
-    ++t;
+    switch (t & 3) {
+      case 0: general(0, t, issued); break;
+      case 1: general(1, t, issued); break;
+      case 2: general(2, t, issued); break;
+      default: general(3, t, issued); break;
+    }
+    finish(t++);
   }
   float ltot[NM];
   wa.row_sums(ltot);
@@ -1617,7 +1725,11 @@ extern "C" int kvhot_paged_attention(
                              a.v_sb, a.v_st, a.v_sh, a.o_st, a.o_sh};
     bool aligned = (ptr_or % 16) == 0;
     for (int64_t x : str) aligned = aligned && (x % al) == 0;
-    if (!aligned) pl.mfma = false;
+    // Buffer descriptors cover one block: its stride (and the token stride
+    // inside it) must fit their 32-bit ranges.
+    const bool fits = a.k_sb > 0 && a.v_sb > 0 && es * a.k_sb < (1LL << 31) && es * a.v_sb < (1LL << 31) &&
+                      a.k_st > 0 && a.v_st > 0 && 16 * es * a.k_st < (1LL << 31) && 16 * es * a.v_st < (1LL << 31);
+    if (!aligned || !fits) pl.mfma = false;
   }
   if (pl.mfma) {
     const int64_t pb = partial_bytes(a.G, head_dim);
