@@ -10,7 +10,11 @@ workload (64 rows, ctx U[128, 2048], 32/8 heads, D=128, bf16, block 16, pool
 
 value = algorithmic bytes moved per step (K/V read + Q in + O out + block
 table + LSE out, plus the append's K/V read+write and slots) / step time, in
-GB/s (1e9).  roofline = one attention call alone (the decode launch plus the
+GB/s (1e9).  prefill = the chunked-prefill rows of the mixed workload (8 x
+512-token chunks on contexts U[0, 4096], 32/8 heads, D=128, bf16): one
+attention call over them, FLOPs counted over visible (query, key) pairs only,
+against the 2.5 PFLOP/s dense bf16 MFMA peak (and the whole mixed batch of
+that workload, decode rows included, timed alongside).  roofline = one attention call alone (the decode launch plus the
 merge launch for rows split across work-groups): its algorithmic bytes over
 its average duration, timed with HIP events on the launch stream across a run
 of back-to-back calls; `traffic` = the HBM bytes rocprofv3's FETCH_SIZE and
@@ -23,6 +27,7 @@ of the same batch.
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload 2]
        python bench.py --copy-probe   # kvhot_copy_blocks of 256 MiB each way
                                       # (counter calibration)
+       python bench.py --prefill-only # the prefill measurement alone
 """
 from __future__ import annotations
 
@@ -39,6 +44,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "attention_decode_gqa64_traffic.md")
 
 
@@ -52,6 +58,9 @@ def parse():
     ap.add_argument("--partition-tokens", type=int, default=0)
     ap.add_argument("--kernel-reps", type=int, default=10, help="passes over all layers for the kernel timing")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-prefill", action="store_true", help="skip the prefill MFMA measurement")
+    ap.add_argument("--prefill-only", action="store_true",
+                    help="only the prefill measurement (for counter runs); prints its JSON object")
     ap.add_argument("--cpu-seconds", type=float, default=20.0, help="budget for the CPU baseline sample")
     ap.add_argument("--copy-probe", action="store_true",
                     help="only run kvhot_copy_blocks over 256 MiB each way, 5 times (counter calibration)")
@@ -98,6 +107,15 @@ def main():
 
     if args.copy_probe:
         copy_probe()
+        return
+    if args.prefill_only:
+        import torch
+
+        torch.cuda.set_device(0)
+        sea = importlib.import_module("serving-engine_amd")
+        wl = importlib.import_module("serving-engine_amd.workloads")
+        print(json.dumps({"prefill": prefill_measure(sea, wl, torch.device("cuda:0"),
+                                                     reps=max(1, args.kernel_reps // 2))}), flush=True)
         return
 
     import torch
@@ -166,6 +184,10 @@ def main():
     torch.cuda.synchronize()
     append_us = start.elapsed_time(end) * 1e3 / (reps * layers)
 
+    prefill = None
+    if not args.no_prefill:
+        prefill = prefill_measure(sea, wl, dev, reps=max(1, args.kernel_reps // 2))
+
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(w, t, layer=0, budget_s=args.cpu_seconds, attn_bytes=attn_bytes + append_bytes)
@@ -211,7 +233,59 @@ def main():
                    "gbs": round(append_bytes / (append_us * 1e-6) / 1e9, 2)},
         "cpu_baseline": cpu,
     }
+    if prefill is not None:
+        line["prefill"] = prefill
     print(json.dumps(line), flush=True)
+
+
+def prefill_measure(sea, wl, dev, reps, layers=16):
+    """One attention call over the prefill rows of the mixed workload, cycled
+    over `layers` pools (so a layer's K/V is not still in the Infinity Cache),
+    timed with HIP events on the launch stream; the whole mixed batch too."""
+    import dataclasses
+
+    import torch
+
+    full = wl.make_workload(3)
+    rows = dataclasses.replace(full, rows=[r for r in full.rows if r.prefill])
+    out = {}
+    for key, w in (("prefill_rows", rows), ("mixed_batch", full)):
+        t = wl.make_tensors(w, dev, num_layers=layers)
+        cache = sea._PagedKVCache(t.kv_cache)
+        meta = sea.build_paged_batch_metadata(w.scheduler_output(), device=dev)
+        blocks = [cache.blocks(i) for i in range(layers)]
+        scale = 1.0 / math.sqrt(w.head_dim)
+
+        def run():
+            for i in range(layers):
+                sea.paged_flash_attention(t.q, blocks[i][0], blocks[i][1], meta, w.num_q_heads,
+                                          w.num_kv_heads, scale)
+
+        run()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            run()
+        e1.record()
+        torch.cuda.synchronize()
+        out[key] = e0.elapsed_time(e1) * 1e3 / (reps * layers)
+        del t, cache, blocks
+        torch.cuda.empty_cache()
+    flops = rows.prefill_flops()
+    tflops = flops / (out["prefill_rows"] * 1e-6) / 1e12
+    return {
+        "workload": full.name,
+        "kernel": "attn_prefill_kernel<BF16,128,2> (8 prefill rows only)",
+        "bound": "mfma",
+        "flops_per_call": flops,
+        "avg_call_us": round(out["prefill_rows"], 3),
+        "achieved": round(tflops, 1),
+        "peak": MFMA_BF16_PEAK_TFLOPS,
+        "unit": "TFLOP/s",
+        "frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4),
+        "mixed_batch_call_us": round(out["mixed_batch"], 3),
+    }
 
 
 def cpu_baseline(w, t, layer, budget_s, attn_bytes):

@@ -129,6 +129,17 @@ class Workload:
         btb = sum(math.ceil(x.k_len / self.block_size) for x in self.rows) * 4
         return kv + qo + btb + t * self.num_q_heads * 4
 
+    def prefill_flops(self) -> int:
+        """FLOPs of the prefill rows (q_len >= 2) counting only visible
+        (query, key) pairs: 4 * Hq * D per pair (QK^T and PV)."""
+        pairs = 0
+        for x in self.rows:
+            if x.q_len < 2:
+                continue
+            for i in range(x.q_len):
+                pairs += max(0, min(x.k_len, x.q_pos_offset + i + 1))
+        return 4 * self.num_q_heads * self.head_dim * pairs
+
     def append_bytes(self) -> int:
         """Algorithmic bytes of the KV append: read K/V + write K/V + slots."""
         es = torch.empty((), dtype=self.dtype).element_size()
