@@ -14,7 +14,14 @@ GB/s (1e9).  prefill = the chunked-prefill rows of the mixed workload (8 x
 512-token chunks on contexts U[0, 4096], 32/8 heads, D=128, bf16): one
 attention call over them, FLOPs counted over visible (query, key) pairs only,
 against the 2.5 PFLOP/s dense bf16 MFMA peak (and the whole mixed batch of
-that workload, decode rows included, timed alongside).  roofline = one attention call alone (the decode launch plus the
+that workload, decode rows included, timed alongside).  engine = output
+tokens/s of greedy decode steps of a random-weight Llama-3.1-8B-shaped model
+(32 layers, hidden 4096, 32/8 heads, D=128, vocab 128256, bf16) whose
+attention is paged|hip over a paged pool, 64 sequences with contexts
+U[128, 2048] (the GQA decode workload's lengths; the context K/V are
+synthetic, every decode step runs the whole model), with the same model on
+the host CPU (fewer layers, the reference's eager attention restated in
+oracle/eager.py) as its baseline.  roofline = one attention call alone (the decode launch plus the
 merge launch for rows split across work-groups): its algorithmic bytes over
 its average duration, timed with HIP events on the launch stream across a run
 of back-to-back calls; `traffic` = the HBM bytes rocprofv3's FETCH_SIZE and
@@ -61,6 +68,10 @@ def parse():
     ap.add_argument("--no-prefill", action="store_true", help="skip the prefill MFMA measurement")
     ap.add_argument("--prefill-only", action="store_true",
                     help="only the prefill measurement (for counter runs); prints its JSON object")
+    ap.add_argument("--no-engine", action="store_true", help="skip the engine tokens/s measurement")
+    ap.add_argument("--engine-only", action="store_true", help="only the engine measurement")
+    ap.add_argument("--engine-steps", type=int, default=16)
+    ap.add_argument("--engine-cpu-layers", type=int, default=2)
     ap.add_argument("--cpu-seconds", type=float, default=20.0, help="budget for the CPU baseline sample")
     ap.add_argument("--copy-probe", action="store_true",
                     help="only run kvhot_copy_blocks over 256 MiB each way, 5 times (counter calibration)")
@@ -107,6 +118,14 @@ def main():
 
     if args.copy_probe:
         copy_probe()
+        return
+    if args.engine_only:
+        import torch
+
+        torch.cuda.set_device(0)
+        print(json.dumps({"engine": engine_measure(torch.device("cuda:0"), steps=args.engine_steps,
+                                                   cpu_layers=0 if args.no_cpu_baseline else args.engine_cpu_layers)}),
+              flush=True)
         return
     if args.prefill_only:
         import torch
@@ -192,6 +211,13 @@ def main():
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(w, t, layer=0, budget_s=args.cpu_seconds, attn_bytes=attn_bytes + append_bytes)
 
+    engine = None
+    if not args.no_engine:
+        del t, cache, blocks
+        torch.cuda.empty_cache()
+        engine = engine_measure(dev, steps=args.engine_steps,
+                                cpu_layers=0 if args.no_cpu_baseline else args.engine_cpu_layers)
+
     line = {
         "metric": "decode paged-attn HBM GB/s (% of 8 TB/s); engine output tokens/sec",
         "value": round(value, 2),
@@ -235,7 +261,205 @@ def main():
     }
     if prefill is not None:
         line["prefill"] = prefill
+    if engine is not None:
+        line["engine"] = engine
     print(json.dumps(line), flush=True)
+
+
+class _DecodeRow:
+    """A decode request as the metadata builder reads it (duck-typed Request:
+    total_len, block_table, phase, num_computed_tokens, request_id)."""
+
+    def __init__(self, rid, total_len, table, phase):
+        self.request_id = rid
+        self.total_len = total_len
+        self.num_computed_tokens = total_len - 1
+        self.block_table = table
+        self.phase = phase
+
+
+def _llama_8b_config(num_layers):
+    from transformers import LlamaConfig
+
+    return LlamaConfig(vocab_size=128256, hidden_size=4096, intermediate_size=14336, num_hidden_layers=num_layers,
+                       num_attention_heads=32, num_key_value_heads=8, head_dim=128,
+                       max_position_embeddings=131072, rms_norm_eps=1e-5, rope_theta=500000.0,
+                       rope_scaling={"rope_type": "llama3", "factor": 8.0, "low_freq_factor": 1.0,
+                                     "high_freq_factor": 4.0, "original_max_position_embeddings": 8192},
+                       tie_word_embeddings=False)
+
+
+def _random_llama(cfg, device, attn_impl):
+    """LlamaForCausalLM in bf16 on `device`, built on the meta device and
+    materialised without the library's initialisation; every weight is
+    filled by tiling one seeded N(0, 0.02) block of 2^20 values (a timing
+    model: the values only need to be finite and of a realistic scale)."""
+    import torch
+    from transformers import LlamaForCausalLM
+
+    cfg._attn_implementation = attn_impl
+    prev = torch.get_default_dtype()
+    torch.set_default_dtype(torch.bfloat16)
+    try:
+        with torch.device("meta"):
+            model = LlamaForCausalLM(cfg)
+    finally:
+        torch.set_default_dtype(prev)
+    model = model.to_empty(device=device)
+    model.eval()
+    gen = torch.Generator(device=device)
+    gen.manual_seed(7)
+    block = torch.empty(1 << 20, dtype=torch.float32, device=device).normal_(0.0, 0.02, generator=gen)
+    block = block.to(torch.bfloat16)
+    with torch.no_grad():
+        for prm in model.parameters():
+            flat = prm.view(-1)
+            for o in range(0, flat.numel(), block.numel()):
+                m = min(block.numel(), flat.numel() - o)
+                flat[o:o + m].copy_(block[:m])
+    # Buffers (the rotary frequencies) are computed, not initialised weights:
+    # rebuild that module on the device.
+    from transformers.models.llama.modeling_llama import LlamaRotaryEmbedding
+
+    with torch.device(device):
+        model.model.rotary_emb = LlamaRotaryEmbedding(config=cfg)
+    return model
+
+
+def _decode_batch(steps, seed=1002):
+    """Context lengths of the GQA decode workload (64 x U[128, 2048], same
+    seed) and shuffled block tables with room for `steps` more tokens."""
+    import numpy as np
+
+    rng = np.random.default_rng(seed)
+    ctx = rng.integers(128, 2048, size=64, endpoint=True)
+    need = [math.ceil((int(c) + steps) / 16) for c in ctx]
+    n = math.ceil(1.25 * sum(need))
+    perm = rng.permutation(n)
+    tables, k = [], 0
+    for nb in need:
+        tables.append([int(b) for b in perm[k:k + nb]])
+        k += nb
+    return [int(c) for c in ctx], tables, n
+
+
+def engine_measure(dev, steps=16, warmup=2, cpu_layers=2):
+    """Greedy decode steps of the random-weight Llama-3.1-8B-shaped model on
+    paged|hip attention: output tokens/s over `steps` timed steps (metadata,
+    append, attention, the whole forward and argmax each step)."""
+    import torch
+
+    sea = importlib.import_module("serving-engine_amd")
+    layers = 32
+    cfg = _llama_8b_config(layers)
+    model = _random_llama(cfg, dev, sea.register_attention())
+    ctx, tables, n = _decode_batch(warmup + steps)
+    kv = sea.allocate_kv_cache(layers, n, 8, 128, dtype=torch.bfloat16, device=dev)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(1002)
+    for lyr in range(layers):  # synthetic context K/V, N(0, 1) / sqrt(128)
+        kv[lyr].normal_(0.0, 1.0 / math.sqrt(128), generator=gen)
+    cache = sea._PagedKVCache(kv)
+    lens = list(ctx)
+    tok = torch.zeros(len(lens), dtype=torch.int64, device=dev)
+
+    def step():
+        nonlocal tok
+        so = sea.SchedulerOutput()
+        for i, (ln, tb) in enumerate(zip(lens, tables)):
+            so.scheduled_requests.append(_DecodeRow(f"s{i}", ln + 1, tb, sea.RequestPhase.NEEDS_DECODE))
+        meta = sea.build_paged_batch_metadata(so, device=dev)
+        with torch.no_grad():
+            out = model(input_ids=tok.view(1, -1), position_ids=meta["positions"].view(1, -1), cache=cache,
+                        write_index=meta["slot_mapping"], paged_metadata=meta, use_cache=False)
+        tok = out.logits[0].argmax(-1)
+        for i in range(len(lens)):
+            lens[i] += 1
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record()
+    for _ in range(steps):
+        step()
+    e1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms = e0.elapsed_time(e1) / steps
+    res = {
+        "model": "Llama-3.1-8B-shaped, random N(0,0.02) weights, bf16: 32 layers, hidden 4096, ffn 14336, "
+                 "32/8 heads, D=128, vocab 128256",
+        "attention": "paged|hip (kvhot_reshape_and_cache + kvhot_paged_attention per layer)",
+        "batch": len(lens),
+        "context": "64 x U[128, 2048] tokens at the first step (synthetic K/V), +1 per step",
+        "steps": steps,
+        "ms_per_step": round(ms, 3),
+        "tokens_per_s": round(len(lens) / (ms * 1e-3), 1),
+        "wall_tokens_per_s": round(len(lens) * steps / wall, 1),
+    }
+    del model, kv, cache
+    torch.cuda.empty_cache()
+    if cpu_layers > 0:
+        res["cpu_baseline"] = engine_cpu_baseline(cpu_layers, ctx, tables, n)
+    return res
+
+
+def engine_cpu_baseline(num_layers, ctx, tables, n, steps=2):
+    """The same decode step on the host CPU with `num_layers` layers and the
+    reference's eager paged attention (restated in oracle/eager.py, per-row
+    form) as the attention function: output tokens/s of that model."""
+    import torch
+    from transformers import AttentionInterface
+
+    from oracle import eager
+
+    sea = importlib.import_module("serving-engine_amd")
+
+    def cpu_attention(module, query, key, value, attention_mask, scaling, **kw):
+        kc, vc = kw["cache"].blocks(module.layer_idx)
+        q = query[0].transpose(0, 1)
+        o = eager.eager_step(q, key[0].transpose(0, 1), value[0].transpose(0, 1), kc, vc, kw["write_index"],
+                             kw["rows"], scaling, kc.shape[2], per_row=True)
+        return o.unsqueeze(0), None
+
+    AttentionInterface.register("paged|eager_cpu", cpu_attention)
+    cfg = _llama_8b_config(num_layers)
+    model = _random_llama(cfg, torch.device("cpu"), "paged|eager_cpu")
+    kv = torch.randn(num_layers, 2, n, 16, 8, 128, dtype=torch.float32).div_(math.sqrt(128)).to(torch.bfloat16)
+    cache = sea._PagedKVCache.__new__(sea._PagedKVCache)  # CPU pool: only .blocks() is used here
+    cache.kv_cache, cache.num_kv_heads, cache.head_dim = kv, 8, 128
+    lens = list(ctx)
+    tok = torch.zeros(len(lens), dtype=torch.int64)
+
+    def step():
+        nonlocal tok
+        rows = [(1, ln + 1, ln, tb) for ln, tb in zip(lens, tables)]
+        slots = torch.tensor([tb[ln // 16] * 16 + ln % 16 for ln, tb in zip(lens, tables)], dtype=torch.int64)
+        pos = torch.tensor(lens, dtype=torch.int64).view(1, -1)
+        with torch.no_grad():
+            out = model(input_ids=tok.view(1, -1), position_ids=pos, cache=cache, write_index=slots, rows=rows,
+                        use_cache=False)
+        tok = out.logits[0].argmax(-1)
+        for i in range(len(lens)):
+            lens[i] += 1
+
+    step()  # warm-up
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    sec = (time.perf_counter() - t0) / steps
+    return {
+        "tokens_per_s": round(len(lens) / sec, 2),
+        "unit": "tokens/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": f"{num_layers}-layer model of the same shape on the host CPU (bf16, torch), batch {len(lens)}, "
+                  f"eager paged attention (per-row form), mean of {steps} steps after 1 warm-up; "
+                  f"{sec * 1e3:.0f} ms per step",
+        "layers": num_layers,
+    }
 
 
 def prefill_measure(sea, wl, dev, reps, layers=16):
