@@ -36,6 +36,7 @@
 #include <algorithm>
 #include <cfloat>
 #include <climits>
+#include <mutex>
 #include <type_traits>
 #include <vector>
 
@@ -1531,10 +1532,78 @@ static void launch_decode(const AttnArgs& a, int64_t rows, int64_t n_dec, hipStr
   hipLaunchKernelGGL((attn_decode_kernel<TT, D, W>), grid, dim3(64 * W), lds, stream, da);
 }
 
+// A second stream per device, so a mixed batch's prefill launch (MFMA-bound,
+// long) and its decode launches (HBM-bound) can share the GPU: the prefill
+// work-groups are dispatched first and the decode work-groups take the CUs
+// the prefill tail frees.  Forked from and joined back into the caller's
+// stream with events (the call stays ordered on that stream, and the pattern
+// is the one stream capture records).  Default priority.
+struct AuxStream {
+  hipStream_t stream = nullptr;
+  hipEvent_t fork = nullptr, join = nullptr;
+};
+static std::mutex g_aux_mutex;
+constexpr int kMaxDevices = 64;
+static AuxStream g_aux[kMaxDevices];
+
+// The current device's aux stream, created on first use; null if that fails
+// (the caller then launches everything on its own stream).  Call with
+// g_aux_mutex held.
+static AuxStream* aux_stream() {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    (void)hipGetLastError();
+    return nullptr;
+  }
+  AuxStream& x = g_aux[dev];
+  if (!x.stream) {
+    hipStream_t st = nullptr;
+    hipEvent_t f = nullptr, j = nullptr;
+    if (hipStreamCreateWithFlags(&st, hipStreamNonBlocking) != hipSuccess ||
+        hipEventCreateWithFlags(&f, hipEventDisableTiming) != hipSuccess ||
+        hipEventCreateWithFlags(&j, hipEventDisableTiming) != hipSuccess) {
+      (void)hipGetLastError();
+      if (f) (void)hipEventDestroy(f);
+      if (st) (void)hipStreamDestroy(st);
+      return nullptr;
+    }
+    x.stream = st;
+    x.fork = f;
+    x.join = j;
+  }
+  return &x;
+}
+
 template <class TT, int D>
 static void launch_mfma(const AttnArgs& a, int waves, int64_t rows, int64_t max_q, int64_t n_dec,
                         int64_t n_pre, int64_t n_merge, hipStream_t stream) {
-  if (!a.sched || n_dec > 0) {
+  const bool dec = !a.sched || n_dec > 0;
+  const bool pre = a.sched ? n_pre > 0 : max_q >= 2;
+  hipStream_t pre_stream = stream;
+  std::unique_lock<std::mutex> lock(g_aux_mutex, std::defer_lock);
+  AuxStream* aux = nullptr;
+  if (dec && pre && a.sched) {
+    lock.lock();
+    aux = aux_stream();
+    if (aux && hipEventRecord(aux->fork, stream) == hipSuccess &&
+        hipStreamWaitEvent(aux->stream, aux->fork, 0) == hipSuccess) {
+      pre_stream = aux->stream;
+    } else {
+      (void)hipGetLastError();
+      aux = nullptr;
+    }
+  }
+  if (pre) {
+    constexpr int NM = prefill_nm(D);
+    const int64_t qpw = kPreWaves * 16 * NM / a.G;
+    const int64_t nqb = (max_q + qpw - 1) / qpw;
+    dim3 grid = a.sched ? dim3(static_cast<uint32_t>(n_pre))
+                        : dim3(static_cast<uint32_t>(a.Hkv * nqb), 1u, static_cast<uint32_t>(rows));
+    AttnArgs pa = a;
+    if (a.sched) pa.sched = a.sched + 2 * n_dec;
+    hipLaunchKernelGGL((attn_prefill_kernel<TT, D, NM>), grid, dim3(64 * kPreWaves), 0, pre_stream, pa);
+  }
+  if (dec) {
     if constexpr (D <= 128) {
       if (waves == 16)
         launch_decode<TT, D, 16>(a, rows, n_dec, stream);
@@ -1549,15 +1618,10 @@ static void launch_mfma(const AttnArgs& a, int waves, int64_t rows, int64_t max_
       hipLaunchKernelGGL((attn_merge_kernel<TT, D>), mgrid, dim3(64), 0, stream, a);
     }
   }
-  if (a.sched ? n_pre > 0 : max_q >= 2) {
-    constexpr int NM = prefill_nm(D);
-    const int64_t qpw = kPreWaves * 16 * NM / a.G;
-    const int64_t nqb = (max_q + qpw - 1) / qpw;
-    dim3 grid = a.sched ? dim3(static_cast<uint32_t>(n_pre))
-                        : dim3(static_cast<uint32_t>(a.Hkv * nqb), 1u, static_cast<uint32_t>(rows));
-    AttnArgs pa = a;
-    if (a.sched) pa.sched = a.sched + 2 * n_dec;
-    hipLaunchKernelGGL((attn_prefill_kernel<TT, D, NM>), grid, dim3(64 * kPreWaves), 0, stream, pa);
+  if (aux) {
+    // Join: the caller's stream waits for the prefill launch.  (Errors of
+    // these calls stay pending for the caller's launch check.)
+    if (hipEventRecord(aux->join, aux->stream) == hipSuccess) (void)hipStreamWaitEvent(stream, aux->join, 0);
   }
 }
 
