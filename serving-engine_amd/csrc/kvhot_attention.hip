@@ -302,8 +302,6 @@ struct WaveAttn {
   // no cross-lane reduction and no rescale of O.  m starts at -FLT_MAX, so
   // masked scores (-inf) give P = 0 and the first visible score moves it.
   // sl = scale * log2(e) > 0 (a negative scale is folded into Q).
-  static constexpr int VC = VW < 4 ? 1 : VW / 4;  // 16-byte chunks of V per row and lane
-  static constexpr int VD = VW < 4 ? VW : 4;      // dwords per chunk
 
   // Raw S^T of a tile: lane (n, g) gets keys 4g+j (sc[s][0]) and 16+4g+j
   // (sc[s][1]) of m-row n.
@@ -320,24 +318,6 @@ struct WaveAttn {
 #pragma unroll
         for (int s = 0; s < NM; ++s) sc[s][h] = TT::mfma(kop, qf[s][c], sc[s][h]);
       }
-  }
-
-  // Chunk c of V rows 4g+j and 16+4g+j (j < 4), head_dim values from EPL*n.
-  template <class Tile>
-  __device__ void read_v(const char* vt, int c, uint32_t (&vr)[8][VD]) const {
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int r = 4 * g + (j & 3) + (j < 4 ? 0 : 16);
-      const char* p = VD == 2 ? vt + Tile::offset(r, n >> 1) + 8 * (n & 1)
-                              : vt + Tile::offset(r, (VW / 4) * n + c);
-      if constexpr (VD == 2) {
-        const u32x2 v = *reinterpret_cast<const u32x2*>(p);
-        vr[j][0] = v.x; vr[j][1] = v.y;
-      } else {
-        const u32x4 v = *reinterpret_cast<const u32x4*>(p);
-        vr[j][0] = v.x; vr[j][1] = v.y; vr[j][2] = v.z; vr[j][3] = v.w;
-      }
-    }
   }
 
   // Local (per-lane) max of each m-row's scores, in log2 units, and whether
@@ -376,25 +356,57 @@ struct WaveAttn {
     return big;
   }
 
-  // O^T += V^T . P^T; vr holds chunk 0 of the V rows on entry.
+  // V^T operands of a tile, read with ds_read_b64_tr_b16.  Within a 16-lane
+  // group, lane l of the read gets element l % 4 of the 8-byte pieces the
+  // lanes 4j + l/4 address (j = 0..3).  Lane n (group g) addresses V row
+  // key (4g + n/4, plus 16 for the second read) at head_dim 16e + 4(n % 4), so
+  // it receives V[key 4g+j (+16)][16e + n] for j = 0..3: the A operand of
+  // O^T += V^T . P^T for head_dim rows 16e .. 16e+15, in the key order of P^T
+  // (slots 8g..8g+3 = keys 4g..4g+3, slots 8g+4.. = keys 16+4g..).  VB blocks of
+  // 16 head_dim values from block e0.
+  static constexpr int VB = EPL < 8 ? EPL : 8;
   template <class Tile>
-  __device__ void pv_lds(const char* vt, uint32_t (&vr)[8][VD], const u32x4 (&pb)[NM]) {
+  __device__ void read_vt(const char* vt, int e0, u32x4 (&va)[VB]) const {
+    typedef __attribute__((address_space(3))) s16x4* lds4_t;
+    const int r = 4 * g + (n >> 2);
 #pragma unroll
-    for (int c = 0; c < VC; ++c) {
-      if (c > 0) read_v<Tile>(vt, c, vr);
-#pragma unroll
-      for (int e2 = 0; e2 < 2 * VD; ++e2) {
-        const int e = 2 * VD * c + e2;
-        const int w = e2 >> 1;
-        const uint32_t sel = (e2 & 1) ? 0x07060302u : 0x05040100u;
-        const u32x4 va = {__builtin_amdgcn_perm(vr[1][w], vr[0][w], sel),
-                          __builtin_amdgcn_perm(vr[3][w], vr[2][w], sel),
-                          __builtin_amdgcn_perm(vr[5][w], vr[4][w], sel),
-                          __builtin_amdgcn_perm(vr[7][w], vr[6][w], sel)};
-#pragma unroll
-        for (int s = 0; s < NM; ++s) o[s][e] = TT::mfma(va, pb[s], o[s][e]);
-      }
+    for (int e = 0; e < VB; ++e) {
+      const int d0 = 16 * (e0 + e) + 4 * (n & 3);
+      const char* p = vt + Tile::offset(r, d0 >> 3) + 2 * (d0 & 7);
+      const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds4_t)(p));
+      const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds4_t)(p + 16 * Tile::RB));
+      const u32x2 l2 = __builtin_bit_cast(u32x2, lo), h2 = __builtin_bit_cast(u32x2, hi);
+      va[e] = u32x4{l2.x, l2.y, h2.x, h2.y};
     }
+  }
+
+  // O^T += V^T . P^T with O^T in head_dim blocks: o[s][e] row i is head_dim
+  // 16e + i (lane (n, g) holds 16e + 4g + j of m-row n).  va holds blocks
+  // 0 .. VB-1 on entry.
+  template <class Tile>
+  __device__ void pv_lds(const char* vt, u32x4 (&va)[VB], const u32x4 (&pb)[NM]) {
+#pragma unroll
+    for (int e0 = 0; e0 < EPL; e0 += VB) {
+      if (e0 > 0) read_vt<Tile>(vt, e0, va);
+#pragma unroll
+      for (int e = 0; e < VB; ++e)
+#pragma unroll
+        for (int s = 0; s < NM; ++s) o[s][e0 + e] = TT::mfma(va[e], pb[s], o[s][e0 + e]);
+    }
+  }
+
+  // Final O (q dtype) and natural-log LSE of m-row s in the head_dim-block
+  // layout of pv_lds, to token t.
+  __device__ void store_final_blocks(const AttnArgs& a, int s, int64_t t, float ltot) const {
+    const float inv = ltot > 0.f ? 1.f / ltot : 0.f;
+    st* op = static_cast<st*>(a.o) + t * a.o_st + static_cast<int64_t>(mh[s]) * a.o_sh + 4 * g;
+#pragma unroll
+    for (int e = 0; e < EPL; ++e)
+      *reinterpret_cast<u32x2*>(op + 16 * e) =
+          u32x2{TT::pack2(o[s][e][0] * inv, o[s][e][1] * inv), TT::pack2(o[s][e][2] * inv, o[s][e][3] * inv)};
+    if (a.lse && g == 0)
+      a.lse[t * a.l_st + static_cast<int64_t>(mh[s]) * a.l_sh] =
+          ltot > 0.f ? (m[s] + __log2f(ltot)) * kLn2 : -INFINITY;
   }
 
   // A tile with no masked key whose scores all stay within kLazyRescale of
@@ -403,14 +415,14 @@ struct WaveAttn {
   __device__ bool tile_fast(float sl, const char* kt, const char* vt) {
     f32x4 sc[NM][2];
     qk_lds<Tile>(kt, sc);
-    uint32_t vr[8][VD];
-    read_v<Tile>(vt, 0, vr);
+    u32x4 va[VB];
+    read_vt<Tile>(vt, 0, va);
     u32x4 pb[NM];
     float lsum[NM];
     if (__builtin_amdgcn_ballot_w64(probs(sl, sc, pb, lsum)) != 0) return false;
 #pragma unroll
     for (int s = 0; s < NM; ++s) l[s] += lsum[s];
-    pv_lds<Tile>(vt, vr, pb);
+    pv_lds<Tile>(vt, va, pb);
     return true;
   }
 
@@ -432,8 +444,8 @@ struct WaveAttn {
             sc[s][h][j] = (tk < kstop && tk <= qpos[s]) ? sc[s][h][j] : -INFINITY;
           }
     }
-    uint32_t vr[8][VD];
-    read_v<Tile>(vt, 0, vr);
+    u32x4 va[VB];
+    read_vt<Tile>(vt, 0, va);
     float mloc[NM];
     if (__builtin_amdgcn_ballot_w64(lazy_check(sl, sc, mloc)) != 0) {
       // Move every row's reference to its exact running max and rescale.
@@ -454,7 +466,7 @@ struct WaveAttn {
     probs(sl, sc, pb, lsum);
 #pragma unroll
     for (int s = 0; s < NM; ++s) l[s] += lsum[s];
-    pv_lds<Tile>(vt, vr, pb);
+    pv_lds<Tile>(vt, va, pb);
   }
 
   // Row sums over the four lane groups that share an m-row.
@@ -1150,7 +1162,7 @@ attn_prefill_kernel(const AttnArgs a) {
   wa.row_sums(ltot);
 #pragma unroll
   for (int s = 0; s < NM; ++s)
-    if (wa.mval[s]) wa.store_final(a, s, qs + q0 + wa.mq[s], ltot[s]);
+    if (wa.mval[s]) wa.store_final_blocks(a, s, qs + q0 + wa.mq[s], ltot[s]);
 }
 
 // ----------------------------------------------------------- VALU kernel --
