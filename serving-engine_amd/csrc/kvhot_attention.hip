@@ -956,7 +956,6 @@ __global__ void __launch_bounds__(64 * kPreWaves)
 attn_prefill_kernel(const AttnArgs a) {
   using Tile = PreTile<D>;
   using WA = WaveAttn<TT, D, NM>;
-  using st = uint16_t;
   // Ring slots, K tile then V tile.  Separate arrays: the compiler can tell
   // that reads of one slot do not alias the DMA into another, and so does
   // not wait for every DMA in flight before each LDS read.
