@@ -21,8 +21,8 @@ attention is paged|hip over a paged pool, 64 sequences with contexts
 U[128, 2048] (the GQA decode workload's lengths; the context K/V are
 synthetic, every decode step runs the whole model), with the same model on
 the host CPU (fewer layers, the reference's eager attention restated in
-oracle/eager.py) as its baseline.  roofline = one attention call alone (the decode launch plus the
-merge launch for rows split across work-groups): its algorithmic bytes over
+oracle/eager.py) as its baseline.  roofline = one attention call alone (the decode launch, plus a
+merge launch when the plan cuts a row across work-groups): its algorithmic bytes over
 its average duration, timed with HIP events on the launch stream across a run
 of back-to-back calls; `traffic` = the HBM bytes rocprofv3's FETCH_SIZE and
 WRITE_SIZE counters read for the same call, scaled by what they read for a
@@ -245,8 +245,8 @@ def main():
         "pct_of_hbm_peak": round(100.0 * value / HBM_PEAK_GBS, 2),
         "roofline": {
             "bound": "hbm",
-            "kernel": "one attention call: attn_decode_kernel<BF16,128,16> + attn_merge_kernel<BF16,128> "
-                      "(rows split across work-groups)",
+            "kernel": "one attention call: attn_decode_kernel<BF16,128,16> (+ attn_merge_kernel<BF16,128> "
+                      "when the launch plan cuts a row across work-groups; on this workload it cuts none)",
             "achieved": round(attn_gbs, 2),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",

@@ -36,6 +36,7 @@
 #include <algorithm>
 #include <cfloat>
 #include <climits>
+#include <functional>
 #include <mutex>
 #include <type_traits>
 #include <vector>
@@ -1372,6 +1373,12 @@ struct Piece {
 constexpr int64_t kMinGroupSlicesPerWave = 2;
 // Split pieces shorter than this are not cut off a segment.
 constexpr int64_t kMinPieceSlices = 4;
+// Cost model for choosing a plan that cuts no segment (and so needs no merge
+// launch): the merge launch and its gap cost about kMergeLaunchUs, and a
+// work-group streams K/V at about kDecodeRateGBs / (work-groups) GB/s
+// (measured on MI355X: 5.5-6 TB/s in the decode kernel's steady state).
+constexpr double kMergeLaunchUs = 5.0;
+constexpr double kDecodeRateGBs = 5500.0;
 
 // Decode launch list.  Work-groups of one device-full are given equal numbers
 // of 16-token slices (inside a work-group the waves balance themselves by
@@ -1382,7 +1389,11 @@ constexpr int64_t kMinPieceSlices = 4;
 // shared among its pieces in proportion to their slices, and each wave's
 // starting range is an even share of its piece.  With given_pt > 0 segments
 // are first cut at multiples of given_pt keys and those partitions are never
-// split further.
+// split further.  Otherwise, when that plan cuts some segment, the uncut
+// alternative is tried too: whole segments, longest first, each to the
+// least-loaded work-group with a free wave (LPT).  It is taken when its
+// longest work-group holds fewer extra slices than a merge launch costs
+// (slice_bytes per slice at the per-work-group rate).
 //
 // Per wave two int4: (row | parts << 16, kvh | part << 16, first slice, end
 // slice) and (query token, visible keys, physical block of the first slice
@@ -1392,8 +1403,8 @@ constexpr int64_t kMinPieceSlices = 4;
 static bool plan_decode(const int32_t* q_lens, const int32_t* k_lens, const int32_t* q_offs,
                         const int32_t* q_starts, const int32_t* bt, int64_t bt_stride, int64_t bs,
                         int64_t rows, int64_t Hkv, bool causal, int W, int64_t groups,
-                        int64_t given_pt, std::vector<int4>& dec, std::vector<int4>& mrg,
-                        int64_t& partials) {
+                        int64_t given_pt, int64_t slice_bytes, std::vector<int4>& dec,
+                        std::vector<int4>& mrg, int64_t& partials) {
   dec.clear();
   mrg.clear();
   partials = 0;
@@ -1461,6 +1472,46 @@ static bool plan_decode(const int32_t* q_lens, const int32_t* k_lens, const int3
     }
   }
   close();
+
+  bool any_cut = false;
+  for (int p : seg_parts) any_cut = any_cut || p > 1;
+  if (given_pt == 0 && any_cut) {
+    const int nseg = static_cast<int>(seg_parts.size());
+    std::vector<int64_t> n(nseg);
+    std::vector<int> order(nseg);
+    for (int sg = 0; sg < nseg; ++sg) {
+      n[sg] = (kend[seg_row[sg]] + 15) / 16;
+      order[sg] = sg;
+    }
+    std::stable_sort(order.begin(), order.end(), [&](int x, int y) { return n[x] > n[y]; });
+    const int64_t ng = std::max<int64_t>(std::max<int64_t>(groups, 1), (nseg + W - 1) / W);
+    // Min-heap of (slices, work-group); a work-group leaves it when full.
+    std::vector<std::pair<int64_t, int64_t>> heap;
+    heap.reserve(ng);
+    for (int64_t g2 = 0; g2 < ng; ++g2) heap.emplace_back(0, g2);
+    std::vector<std::vector<Piece>> lpt(ng);
+    int64_t lmax = 0;
+    for (int sg : order) {
+      std::pop_heap(heap.begin(), heap.end(), std::greater<>());
+      auto [ld, g2] = heap.back();
+      lpt[g2].push_back(Piece{seg_row[sg], seg_kvh[sg], 0, static_cast<int>(n[sg]), 0, sg});
+      ld += n[sg];
+      lmax = std::max(lmax, ld);
+      if (static_cast<int>(lpt[g2].size()) < W) {
+        heap.back() = {ld, g2};
+        std::push_heap(heap.begin(), heap.end(), std::greater<>());
+      } else {
+        heap.pop_back();
+      }
+    }
+    const double slice_us = static_cast<double>(slice_bytes) * ng / (kDecodeRateGBs * 1e3);
+    if (static_cast<double>(lmax - target) * slice_us <= kMergeLaunchUs) {
+      wgs.clear();
+      for (auto& g2 : lpt)
+        if (!g2.empty()) wgs.push_back(std::move(g2));
+      std::fill(seg_parts.begin(), seg_parts.end(), 1);
+    }
+  }
 
   // Partial indices of split segments.
   std::vector<int64_t> seg_base(seg_parts.size(), -1);
@@ -1688,8 +1739,8 @@ extern "C" int64_t kvhot_paged_attention_schedule(
     const int64_t G = num_q_heads / num_kv_heads;
     const int64_t groups = resident_decode_waves(dtype, head_dim, pl.waves, G) / pl.waves;
     if (plan_decode(q_lens, k_lens, q_pos_offsets, q_starts, block_table, bt_row_stride, block_size,
-                    num_rows, num_kv_heads, is_causal != 0, pl.waves, groups, partition_tokens, dec,
-                    mrg, partials)) {
+                    num_rows, num_kv_heads, is_causal != 0, pl.waves, groups, partition_tokens,
+                    32 * head_dim * dtype_size(dtype), dec, mrg, partials)) {
       plan_prefill(q_lens, k_lens, q_pos_offsets, num_rows, num_kv_heads, G, head_dim,
                    is_causal != 0, pre);
     } else {  // counts beyond the descriptor fields: no schedule

@@ -225,10 +225,12 @@ def test_schedule_prefill_blocks_longest_first(lib):
     assert list(pre[:, 3]) == sorted(pre[:, 3], reverse=True)
 
 
-def test_schedule_balances_work_groups(lib):
-    """Without a partition size the planner gives every work-group of one
-    device-full (256 work-groups of 16 waves when no device is queried) the
-    same number of slices, splitting ranges only where a cut falls."""
+def test_schedule_uncut_when_balanced(lib):
+    """Many rows of mixed lengths (the 64-row GQA decode shape): whole
+    (row, kv head) segments packed longest first fit one device-full (256
+    work-groups of 16 waves when no device is queried) within a merge
+    launch's worth of slices of the even cut, so no segment is cut and there
+    is no merge launch."""
     import numpy as np
 
     rng = np.random.default_rng(0)
@@ -238,10 +240,24 @@ def test_schedule_balances_work_groups(lib):
     loads = _check_decode_schedule(dec, merge, ws, qs, 16, dict(enumerate(ctx.tolist())), 8)
     total = sum(-(-int(c) // 16) for c in ctx) * 8
     target = -(-total // 256)
+    assert len(merge) == 0 and ws == 0
+    assert len(loads) <= 256
+    # 5 us of merge launch at 8 KiB slices and 5.5 TB/s over 256 work-groups: 13 slices
+    assert max(loads) <= target + 13
+
+
+def test_schedule_cuts_long_rows(lib):
+    """A few long rows cannot fill the device whole: segments are cut into
+    parts of equal work-group loads, joined by merge units, and every cut
+    leaves at least 4 slices on either side."""
+    ctx = [32768] * 4 + [1000, 3000]
+    dec, pre, merge, ws, qs = _schedule(lib, [1] * len(ctx), ctx, [c - 1 for c in ctx])
+    loads = _check_decode_schedule(dec, merge, ws, qs, 16, dict(enumerate(ctx)), 8)
+    total = sum(-(-c // 16) for c in ctx) * 8
+    target = -(-total // 256)
+    assert len(merge) > 0 and ws > 0
     assert len(loads) <= 257
     assert max(loads) <= target + max(2, target // 32)
-    # every cut leaves at least 4 slices on either side
-    assert len(merge) < len(loads)
 
 
 def test_schedule_tiny_rows_and_empty_rows(lib):
