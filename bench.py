@@ -19,9 +19,10 @@ tokens/s of greedy decode steps of a random-weight Llama-3.1-8B-shaped model
 (32 layers, hidden 4096, 32/8 heads, D=128, vocab 128256, bf16) whose
 attention is paged|hip over a paged pool, 64 sequences with contexts
 U[128, 2048] (the GQA decode workload's lengths; the context K/V are
-synthetic, every decode step runs the whole model), with the same model on
-the host CPU (fewer layers, the reference's eager attention restated in
-oracle/eager.py) as its baseline.  roofline = one attention call alone (the decode launch, plus a
+synthetic, every decode step runs the whole model; the step is recorded once
+in a HIP graph and replayed, and the eager step is reported beside it), with
+the same model on the host CPU (fewer layers, the reference's eager attention
+restated in oracle/eager.py) as its baseline.  roofline = one attention call alone (the decode launch, plus a
 merge launch when the plan cuts a row across work-groups): its algorithmic bytes over
 its average duration, timed with HIP events on the launch stream across a run
 of back-to-back calls; `traffic` = the HBM bytes rocprofv3's FETCH_SIZE and
@@ -346,14 +347,16 @@ def _decode_batch(steps, seed=1002):
 def engine_measure(dev, steps=16, warmup=2, cpu_layers=2):
     """Greedy decode steps of the random-weight Llama-3.1-8B-shaped model on
     paged|hip attention: output tokens/s over `steps` timed steps (metadata,
-    append, attention, the whole forward and argmax each step)."""
+    append, attention, the whole forward and argmax each step), run eagerly
+    and then as replays of the step recorded in a HIP graph
+    (DecodeStepGraph), continuing the same sequences."""
     import torch
 
     sea = importlib.import_module("serving-engine_amd")
     layers = 32
     cfg = _llama_8b_config(layers)
     model = _random_llama(cfg, dev, sea.register_attention())
-    ctx, tables, n = _decode_batch(warmup + steps)
+    ctx, tables, n = _decode_batch(2 * (warmup + steps))
     kv = sea.allocate_kv_cache(layers, n, 8, 128, dtype=torch.bfloat16, device=dev)
     gen = torch.Generator(device=dev)
     gen.manual_seed(1002)
@@ -387,6 +390,27 @@ def engine_measure(dev, steps=16, warmup=2, cpu_layers=2):
     e1.record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
+    ms_eager = e0.elapsed_time(e1) / steps
+
+    # The same step recorded once and replayed (continuing the sequences).
+    graph = sea.DecodeStepGraph(model, cache, len(lens), max(len(t) for t in tables), 32, 8, 128, dev)
+    graph.tokens.copy_(tok)
+
+    def gstep():
+        graph.step([ln + 1 for ln in lens], tables)
+        for i in range(len(lens)):
+            lens[i] += 1
+
+    for _ in range(warmup):
+        gstep()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    e0.record()
+    for _ in range(steps):
+        gstep()
+    e1.record()
+    torch.cuda.synchronize()
+    gwall = time.perf_counter() - t0
     ms = e0.elapsed_time(e1) / steps
     res = {
         "model": "Llama-3.1-8B-shaped, random N(0,0.02) weights, bf16: 32 layers, hidden 4096, ffn 14336, "
@@ -395,11 +419,16 @@ def engine_measure(dev, steps=16, warmup=2, cpu_layers=2):
         "batch": len(lens),
         "context": "64 x U[128, 2048] tokens at the first step (synthetic K/V), +1 per step",
         "steps": steps,
+        "step": "recorded once in a HIP graph (DecodeStepGraph) and replayed: per step the host builds the "
+                "metadata and the attention launch list, two pinned copies, one graph launch",
         "ms_per_step": round(ms, 3),
         "tokens_per_s": round(len(lens) / (ms * 1e-3), 1),
-        "wall_tokens_per_s": round(len(lens) * steps / wall, 1),
+        "wall_tokens_per_s": round(len(lens) * steps / gwall, 1),
+        "graph_recordings": graph.recordings,
+        "eager": {"ms_per_step": round(ms_eager, 3), "tokens_per_s": round(len(lens) / (ms_eager * 1e-3), 1),
+                  "wall_tokens_per_s": round(len(lens) * steps / wall, 1)},
     }
-    del model, kv, cache
+    del graph, model, kv, cache
     torch.cuda.empty_cache()
     if cpu_layers > 0:
         res["cpu_baseline"] = engine_cpu_baseline(cpu_layers, ctx, tables, n)

@@ -23,10 +23,12 @@ from .model_runner import (
     register_attention,
     step_inputs,
 )
+from .decode_graph import DecodeStepGraph
 from .request import Request, RequestPhase, SchedulerOutput
 
 __all__ = [
     "BLOCK_SIZE",
+    "DecodeStepGraph",
     "PAGED_K_TILE_SIZE",
     "PAGED_Q_TILE_SIZE",
     "PAGED_HIP_ATTN_IMPL",

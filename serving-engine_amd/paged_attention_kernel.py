@@ -56,6 +56,13 @@ def _workspace(device: torch.device, stream: int, nbytes: int) -> torch.Tensor |
     return ws
 
 
+def schedule_key(device, hq, hkv, d, bs, pt, causal, dtype):
+    """Key of a launch list in metadata["_schedules"]: one per attention
+    shape (head counts, head_dim, block size, partition size, causality and
+    dtype code) on one device."""
+    return (hq, hkv, d, bs, pt, bool(causal), dtype, str(device))
+
+
 def _schedule(metadata, device, hq, hkv, d, bs, pt, causal, dtype):
     """(device units, n_decode, n_prefill, n_merge, workspace bytes) of
     kvhot_paged_attention_schedule for this step, built once per attention
@@ -64,7 +71,7 @@ def _schedule(metadata, device, hq, hkv, d, bs, pt, causal, dtype):
     host_q = metadata.get("host_q_lens")
     if host_q is None:
         return None
-    key = (hq, hkv, d, bs, pt, bool(causal), dtype, str(device))
+    key = schedule_key(device, hq, hkv, d, bs, pt, causal, dtype)
     cache = metadata.setdefault("_schedules", {})
     if key in cache:
         return cache[key]
@@ -253,18 +260,26 @@ def build_paged_batch_metadata(scheduler_output, device="cuda"):
     return meta
 
 
-def build_slot_mapping(metadata, block_size=BLOCK_SIZE):
+def build_slot_mapping(metadata, block_size=BLOCK_SIZE, out=None):
     """(slot_mapping, positions), int64 [total_query], built on the device.
 
     slot = block_table[row, pos // block_size] * block_size + pos % block_size
     for pos = q_pos_offset + i: the write index and RoPE position ids of
     ModelRunner.forward (serving_engine/model_runner.py:127-129, 142-170).
+    ``out`` (extension): a (slots, positions) pair of int64 device tensors of
+    total_query elements to write instead of new ones.
     """
     bt = metadata["block_table"]
     device = bt.device
     total = int(metadata["total_query"])
-    slots = torch.empty(total, dtype=torch.int64, device=device)
-    positions = torch.empty(total, dtype=torch.int64, device=device)
+    if out is None:
+        slots = torch.empty(total, dtype=torch.int64, device=device)
+        positions = torch.empty(total, dtype=torch.int64, device=device)
+    else:
+        slots, positions = out
+        for t in out:
+            if t.dtype != torch.int64 or t.device != device or t.numel() != total or not t.is_contiguous():
+                raise ValueError(f"out tensors must be contiguous int64 [{total}] on {device}")
     r = metadata["q_lens"].shape[0]
     if total == 0 or r == 0:
         return slots, positions
