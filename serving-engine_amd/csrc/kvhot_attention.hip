@@ -96,6 +96,16 @@ __device__ inline void dma16(__amdgpu_buffer_rsrc_t r, void* dst, int off) {
 // lane offset (no 64-bit per-lane address registers), and the hardware returns
 // zeros for any offset past `bytes`.  Word 3 = 0x00020000: raw dword access
 // for CDNA.
+// A pointer every lane holds, broadcast from lane 0 so the compiler keeps it
+// (and descriptors built from it) in scalar registers.
+template <typename T>
+__device__ inline const T* uniform_ptr(const T* p) {
+  const uint64_t v = reinterpret_cast<uint64_t>(p);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v));
+  const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v >> 32));
+  return reinterpret_cast<const T*>((static_cast<uint64_t>(hi) << 32) | lo);
+}
+
 __device__ inline __amdgpu_buffer_rsrc_t block_rsrc(const void* base, int bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, 0x00020000);
 }
@@ -211,6 +221,21 @@ struct WaveAttn {
     const int k_lane = 2 * (n * static_cast<int>(a.k_st) + 8 * g);
     const st* kb = static_cast<const st*>(a.k) + static_cast<int64_t>(kvh) * a.k_sh + id * a.k_sb;
     const st* vb = static_cast<const st*>(a.v) + static_cast<int64_t>(kvh) * a.v_sh + id * a.v_sb;
+    const __amdgpu_buffer_rsrc_t kr = block_rsrc(kb, static_cast<int>(2 * a.k_sb));
+    const __amdgpu_buffer_rsrc_t vr = block_rsrc(vb, static_cast<int>(2 * a.v_sb));
+    const int ks = 2 * bo * static_cast<int>(a.k_st);
+    const int vs = 2 * bo * static_cast<int>(a.v_st);
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+      T.k[c] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(kr, k_lane + 64 * c, ks, 0));
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      buffer_dwords<VW>(vr, 2 * ((4 * g + j) * static_cast<int>(a.v_st) + EPL * n), vs, T.v[j]);
+  }
+
+  // The loads of load_slice from the slice's block bases kb, vb (uniform).
+  __device__ void load_slice_from(const AttnArgs& a, const st* kb, const st* vb, int bo, KVSlice<D>& T) const {
+    const int k_lane = 2 * (n * static_cast<int>(a.k_st) + 8 * g);
     const __amdgpu_buffer_rsrc_t kr = block_rsrc(kb, static_cast<int>(2 * a.k_sb));
     const __amdgpu_buffer_rsrc_t vr = block_rsrc(vb, static_cast<int>(2 * a.v_sb));
     const int ks = 2 * bo * static_cast<int>(a.k_st);
@@ -731,14 +756,20 @@ attn_decode_kernel(const AttnArgs a) {
       live = j >= 0;
     }
     // The next slice's block id is fetched while this slice's loads land.
-    const int64_t jb = j >= 0 ? block_of(krow, j) : 0;
+    const int64_t jb = j >= 0 ? block_of(__builtin_amdgcn_readfirstlane(krow), __builtin_amdgcn_readfirstlane(j)) : 0;
     if (have) {
       wa.compute_slice(a, 16 * i, kkend, INT_MAX, T);
       used = true;
     }
     if (j >= 0) {
       i = j;
-      wa.load_slice(a, kkvh, jb, (16 * j) % bs, T);
+      // The slice's bases and offset are broadcast: they are uniform, but are
+      // carried out of claim loops the compiler cannot prove uniform, and a
+      // per-lane buffer descriptor puts each load in a loop over the distinct
+      // descriptors that waits for the load before it.
+      wa.load_slice_from(a, uniform_ptr(static_cast<const st*>(a.k) + static_cast<int64_t>(kkvh) * a.k_sh + jb * a.k_sb),
+                         uniform_ptr(static_cast<const st*>(a.v) + static_cast<int64_t>(kkvh) * a.v_sh + jb * a.v_sb),
+                         __builtin_amdgcn_readfirstlane((16 * j) % bs), T);
       have = true;
       continue;
     }

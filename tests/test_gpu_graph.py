@@ -80,7 +80,13 @@ def test_decode_graph_replays_match_eager_steps(cuda, sea):
         out = g.step(lens, tables)
         torch.cuda.synchronize()
         torch.testing.assert_close(g.logits.float(), logits_e, atol=5e-2, rtol=2e-2)
-        assert torch.equal(out, tok_e), f"step {s}: tokens differ"
+        # Tokens agree wherever the eager step's top two logits are apart by
+        # more than the tolerance (a near tie may go either way: the
+        # attention's summation order is set at run time).
+        top2 = logits_e.topk(2, dim=-1).values
+        clear = (top2[:, 0] - top2[:, 1]) > 0.1
+        assert torch.equal(out[clear], tok_e[clear]), f"step {s}: tokens differ"
+        g.tokens.copy_(tok_e)  # both continue from the eager tokens
         tok = tok_e
         lens = [x + 1 for x in lens]
     assert g.recordings >= 2  # the long row's step recorded again (and the next step back)
