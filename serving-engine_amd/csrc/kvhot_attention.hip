@@ -1410,6 +1410,17 @@ constexpr int64_t kMinPieceSlices = 4;
 // (measured on MI355X: 5.5-6 TB/s in the decode kernel's steady state).
 constexpr double kMergeLaunchUs = 5.0;
 constexpr double kDecodeRateGBs = 5500.0;
+// Kv heads stream at different rates: which HBM channels a head's rows hit
+// follows from the row's byte offset inside a token's [Hkv, D] row, and on
+// MI355X two of eight 256-byte offsets read about 16% slower in every XCD
+// (shifting the pool by 256 bytes moves the slow heads along).  A work-group
+// of one head's segments then ends late or early with its head; one that
+// holds a mix of heads averages the rates (its waves share the slices).  So
+// the packing below places a segment, among the up to kMixCandidates
+// work-groups within kMixSlack slices of the least loaded, in the one that
+// holds the fewest segments of its kv head.
+constexpr int kMixCandidates = 8;
+constexpr int64_t kMixSlack = 2;
 
 // Decode launch list.  Work-groups of one device-full are given equal numbers
 // of 16-token slices (inside a work-group the waves balance themselves by
@@ -1521,18 +1532,37 @@ static bool plan_decode(const int32_t* q_lens, const int32_t* k_lens, const int3
     heap.reserve(ng);
     for (int64_t g2 = 0; g2 < ng; ++g2) heap.emplace_back(0, g2);
     std::vector<std::vector<Piece>> lpt(ng);
+    std::vector<int> held(static_cast<size_t>(ng * Hkv), 0);  // segments of each kv head per work-group
+    std::vector<std::pair<int64_t, int64_t>> cand;
     int64_t lmax = 0;
     for (int sg : order) {
+      const int h = seg_kvh[sg];
+      cand.clear();
       std::pop_heap(heap.begin(), heap.end(), std::greater<>());
-      auto [ld, g2] = heap.back();
+      cand.push_back(heap.back());
+      heap.pop_back();
+      while (static_cast<int>(cand.size()) < kMixCandidates && !heap.empty() &&
+             heap.front().first <= cand[0].first + kMixSlack) {
+        std::pop_heap(heap.begin(), heap.end(), std::greater<>());
+        cand.push_back(heap.back());
+        heap.pop_back();
+      }
+      size_t c = 0;
+      for (size_t k = 1; k < cand.size(); ++k)
+        if (held[cand[k].second * Hkv + h] < held[cand[c].second * Hkv + h]) c = k;
+      for (size_t k = 0; k < cand.size(); ++k) {
+        if (k == c) continue;
+        heap.push_back(cand[k]);
+        std::push_heap(heap.begin(), heap.end(), std::greater<>());
+      }
+      auto [ld, g2] = cand[c];
       lpt[g2].push_back(Piece{seg_row[sg], seg_kvh[sg], 0, static_cast<int>(n[sg]), 0, sg});
+      ++held[g2 * Hkv + h];
       ld += n[sg];
       lmax = std::max(lmax, ld);
       if (static_cast<int>(lpt[g2].size()) < W) {
-        heap.back() = {ld, g2};
+        heap.push_back({ld, g2});
         std::push_heap(heap.begin(), heap.end(), std::greater<>());
-      } else {
-        heap.pop_back();
       }
     }
     const double slice_us = static_cast<double>(slice_bytes) * ng / (kDecodeRateGBs * 1e3);

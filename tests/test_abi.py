@@ -246,6 +246,26 @@ def test_schedule_uncut_when_balanced(lib):
     assert max(loads) <= target + 13
 
 
+def test_schedule_uncut_mixes_kv_heads(lib):
+    """Whole-segment packing spreads each row's kv heads over work-groups so
+    that every work-group holds several heads (kv heads stream at different
+    rates, and a work-group of one head would end with its head's rate): 256
+    rows of about 1000 tokens give every work-group all 8 heads, 64 rows of
+    128-2048 tokens two heads per work-group, with the same load bound."""
+    import numpy as np
+
+    rng = np.random.default_rng(1)
+    for lo, hi, rows, want in ((1000, 1100, 256, 8), (128, 2048, 64, 2)):
+        ctx = rng.integers(lo, hi, size=rows, endpoint=True)
+        dec, pre, merge, ws, qs = _schedule(lib, [1] * rows, ctx, ctx - 1)
+        loads = _check_decode_schedule(dec, merge, ws, qs, 16, dict(enumerate(ctx.tolist())), 8)
+        assert len(merge) == 0
+        total = sum(-(-int(c) // 16) for c in ctx) * 8
+        assert max(loads) <= -(-total // 256) + 13
+        heads = [len({w["kvh"] for w in dec[g:g + 16] if w}) for g in range(0, len(dec), 16)]
+        assert min(heads) >= want, (rows, sorted(set(heads)))
+
+
 def test_schedule_cuts_long_rows(lib):
     """A few long rows cannot fill the device whole: segments are cut into
     parts of equal work-group loads, joined by merge units, and every cut
