@@ -1472,45 +1472,55 @@ static bool plan_decode(const int32_t* q_lens, const int32_t* k_lens, const int3
   };
   std::vector<int> seg_parts;  // parts per segment (row, kv head)
   std::vector<int> seg_row, seg_kvh;
+  // Adds slices [s, s + rem) of segment seg (row r, kv head h) to the open
+  // work-groups: whole when it is a fixed partition p, else cut at the
+  // work-group loads.
+  auto place = [&](int seg, int64_t r, int64_t h, int64_t s, int64_t rem, int64_t p, bool splittable) {
+    for (;;) {
+      if (static_cast<int>(cur.size()) == W) close();
+      const int64_t space = target - load;
+      if (rem <= space + slack || (!splittable && cur.empty())) {
+        const int part = splittable ? seg_parts[seg]++ : static_cast<int>(p);
+        cur.push_back(Piece{static_cast<int>(r), static_cast<int>(h), static_cast<int>(s),
+                            static_cast<int>(s + rem), part, seg});
+        load += rem;
+        return;
+      }
+      if (!splittable || space < kMinPieceSlices) {
+        close();
+        continue;
+      }
+      int64_t take = space;
+      if (rem - take < kMinPieceSlices) take = rem - kMinPieceSlices;
+      cur.push_back(Piece{static_cast<int>(r), static_cast<int>(h), static_cast<int>(s),
+                          static_cast<int>(s + take), seg_parts[seg]++, seg});
+      s += take;
+      rem -= take;
+      close();
+    }
+  };
+  const int64_t pt_sl = given_pt > 0 ? given_pt / 16 : 0;
   for (int64_t r = 0; r < rows; ++r) {
     if (kend[r] < 0) continue;
     const int64_t n = (kend[r] + 15) / 16;
-    const int64_t pt_sl = given_pt > 0 ? given_pt / 16 : 0;
+    const int seg0 = static_cast<int>(seg_parts.size());
     for (int64_t h = 0; h < Hkv; ++h) {
-      const int seg = static_cast<int>(seg_parts.size());
       seg_parts.push_back(0);
       seg_row.push_back(static_cast<int>(r));
       seg_kvh.push_back(static_cast<int>(h));
-      // Atoms: the fixed partitions, or the whole segment (splittable).
-      const int64_t natoms = pt_sl > 0 ? std::max<int64_t>((n + pt_sl - 1) / pt_sl, 1) : 1;
+    }
+    if (pt_sl > 0) {
+      // Fixed partitions, partition-major over the row's kv heads: a
+      // work-group's run of partitions spans the heads, whose streaming
+      // rates differ (see kMixCandidates).
+      const int64_t natoms = std::max<int64_t>((n + pt_sl - 1) / pt_sl, 1);
       for (int64_t p = 0; p < natoms; ++p) {
-        int64_t s = pt_sl > 0 ? p * pt_sl : 0;
-        int64_t rem = (pt_sl > 0 ? std::min(n, s + pt_sl) : n) - s;
-        const bool splittable = pt_sl == 0;
-        for (;;) {
-          if (static_cast<int>(cur.size()) == W) close();
-          const int64_t space = target - load;
-          if (rem <= space + slack || (!splittable && cur.empty())) {
-            const int part = splittable ? seg_parts[seg]++ : static_cast<int>(p);
-            cur.push_back(Piece{static_cast<int>(r), static_cast<int>(h), static_cast<int>(s),
-                                static_cast<int>(s + rem), part, seg});
-            load += rem;
-            break;
-          }
-          if (!splittable || space < kMinPieceSlices) {
-            close();
-            continue;
-          }
-          int64_t take = space;
-          if (rem - take < kMinPieceSlices) take = rem - kMinPieceSlices;
-          cur.push_back(Piece{static_cast<int>(r), static_cast<int>(h), static_cast<int>(s),
-                              static_cast<int>(s + take), seg_parts[seg]++, seg});
-          s += take;
-          rem -= take;
-          close();
-        }
+        const int64_t s = p * pt_sl;
+        for (int64_t h = 0; h < Hkv; ++h) place(seg0 + static_cast<int>(h), r, h, s, std::min(n, s + pt_sl) - s, p, false);
       }
-      if (pt_sl > 0) seg_parts[seg] = static_cast<int>(natoms);
+      for (int64_t h = 0; h < Hkv; ++h) seg_parts[seg0 + h] = static_cast<int>(natoms);
+    } else {
+      for (int64_t h = 0; h < Hkv; ++h) place(seg0 + static_cast<int>(h), r, h, 0, n, 0, true);
     }
   }
   close();
