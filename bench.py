@@ -24,8 +24,10 @@ in a HIP graph and replayed, and the eager step is reported beside it), with
 the same model on the host CPU (fewer layers, the reference's eager attention
 restated in oracle/eager.py) as its baseline.  roofline = one attention call alone (the decode launch, plus a
 merge launch when the plan cuts a row across work-groups): its algorithmic bytes over
-its average duration, timed with HIP events on the launch stream across a run
-of back-to-back calls; `traffic` = the HBM bytes rocprofv3's FETCH_SIZE and
+its average duration, timed with HIP events on the launch stream across
+replays of one recorded HIP graph of 32 back-to-back calls (device time per
+launch; the eager per-call time, host dispatch included, is reported beside
+it); `traffic` = the HBM bytes rocprofv3's FETCH_SIZE and
 WRITE_SIZE counters read for the same call, scaled by what they read for a
 copy of known size, as recorded in profiles/attention_decode_gqa64_traffic.md
 (null when that file is absent).  cpu_baseline = the reference's eager
@@ -182,27 +184,42 @@ def main():
     step_bytes = layers * (attn_bytes + append_bytes)
     value = step_bytes / (ms_per_step * 1e-3) / 1e9
 
-    # Attention kernel alone: back-to-back launches over the layers.
+    # Attention and append alone: back-to-back launches over the layers, as
+    # eager calls (host dispatch included) and as replays of one recorded HIP
+    # graph of the same launches (device time per launch: the figure the
+    # kernel trace's average is compared with).
     reps = max(1, args.kernel_reps)
-    torch.cuda.synchronize()
-    start.record()
-    for _ in range(reps):
-        for i in range(layers):
-            attention(i)
-    end.record()
-    torch.cuda.synchronize()
-    attn_us = start.elapsed_time(end) * 1e3 / (reps * layers)
-    attn_gbs = attn_bytes / (attn_us * 1e-6) / 1e9
 
-    # Append alone.
-    torch.cuda.synchronize()
-    start.record()
-    for _ in range(reps):
-        for i in range(layers):
-            cache.write(t.new_k, t.new_v, i, slots)
-    end.record()
-    torch.cuda.synchronize()
-    append_us = start.elapsed_time(end) * 1e3 / (reps * layers)
+    def per_launch_us(body):
+        torch.cuda.synchronize()
+        start.record()
+        for _ in range(reps):
+            body()
+        end.record()
+        torch.cuda.synchronize()
+        eager = start.elapsed_time(end) * 1e3 / (reps * layers)
+        graph = torch.cuda.CUDAGraph()
+        side = torch.cuda.Stream(dev)
+        side.wait_stream(torch.cuda.current_stream(dev))
+        with torch.cuda.stream(side):
+            body()  # every lazy set-up done before the recording
+        torch.cuda.current_stream(dev).wait_stream(side)
+        torch.cuda.synchronize()
+        with torch.cuda.graph(graph):
+            body()
+        graph.replay()
+        torch.cuda.synchronize()
+        start.record()
+        for _ in range(reps):
+            graph.replay()
+        end.record()
+        torch.cuda.synchronize()
+        return start.elapsed_time(end) * 1e3 / (reps * layers), eager
+
+    attn_us, attn_eager_us = per_launch_us(lambda: [attention(i) for i in range(layers)])
+    attn_gbs = attn_bytes / (attn_us * 1e-6) / 1e9
+    append_us, append_eager_us = per_launch_us(
+        lambda: [cache.write(t.new_k, t.new_v, i, slots) for i in range(layers)])
 
     prefill = None
     if not args.no_prefill:
@@ -255,8 +272,11 @@ def main():
             "traffic": recorded_traffic(args.workload),
             "algorithmic_bytes_per_launch": attn_bytes,
             "avg_launch_us": round(attn_us, 3),
+            "avg_launch_us_timing": "HIP events over replays of one recorded graph of the 32 back-to-back calls",
+            "eager_call_us": round(attn_eager_us, 3),
         },
-        "append": {"avg_launch_us": round(append_us, 3), "algorithmic_bytes": append_bytes,
+        "append": {"avg_launch_us": round(append_us, 3), "eager_call_us": round(append_eager_us, 3),
+                   "algorithmic_bytes": append_bytes,
                    "gbs": round(append_bytes / (append_us * 1e-6) / 1e9, 2)},
         "cpu_baseline": cpu,
     }

@@ -21,35 +21,45 @@ void clear_error() { g_last_error.clear(); }
 // ------------------------------------------------------------------ append --
 
 // One lane copies one W-sized unit of one (token, head) row, for K (kv = 0) or
-// V (kv = 1).  Strides are in units of W.
-template <typename W, typename SlotT>
+// V (kv = 1).  Strides are in units of W.  Lane indices and slots are of type
+// I: 32-bit (cheaper divisions) whenever the call's units and the pool's
+// slots fit.
+template <typename W, typename SlotT, typename I>
 __global__ void __launch_bounds__(256)
 reshape_and_cache_kernel(const W* __restrict__ key, const W* __restrict__ value,
                          W* __restrict__ k_cache, W* __restrict__ v_cache,
-                         const SlotT* __restrict__ slots, int64_t num_tokens,
-                         int32_t num_heads, int32_t units_per_row,
-                         int64_t k_st, int64_t k_sh, int64_t v_st, int64_t v_sh,
-                         int64_t kc_sb, int64_t kc_st, int64_t kc_sh,
+                         const SlotT* __restrict__ slots, I per_kv, I num_heads,
+                         I units_per_row, int64_t k_st, int64_t k_sh, int64_t v_st,
+                         int64_t v_sh, int64_t kc_sb, int64_t kc_st, int64_t kc_sh,
                          int64_t vc_sb, int64_t vc_st, int64_t vc_sh,
                          int32_t block_size, int64_t num_slots) {
-  const int64_t per_kv = num_tokens * num_heads * units_per_row;
-  int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  I idx = static_cast<I>(blockIdx.x) * static_cast<I>(blockDim.x) + static_cast<I>(threadIdx.x);
   if (idx >= 2 * per_kv) return;
-  const int kv = idx >= per_kv;
+  const bool kv = idx >= per_kv;
   if (kv) idx -= per_kv;
-  const int32_t u = static_cast<int32_t>(idx % units_per_row);
-  const int64_t th = idx / units_per_row;
-  const int32_t h = static_cast<int32_t>(th % num_heads);
-  const int64_t t = th / num_heads;
+  const I u = idx % units_per_row;
+  const I th = idx / units_per_row;
+  const int64_t h = static_cast<int64_t>(th % num_heads);
+  const int64_t t = static_cast<int64_t>(th / num_heads);
+  // The unit and its token's slot are loaded together (the unit's address
+  // does not depend on the slot), so the store waits for one round trip.
+  W x = kv ? value[t * v_st + h * v_sh + u] : key[t * k_st + h * k_sh + u];
   const int64_t s = static_cast<int64_t>(slots[t]);
+  __asm__ volatile("" : "+v"(x));  // keeps the load ahead of the slot test
   if (s < 0 || s >= num_slots) return;
-  const int64_t blk = s / block_size;
-  const int64_t off = s - blk * block_size;
-  if (kv == 0) {
-    k_cache[blk * kc_sb + off * kc_st + h * kc_sh + u] = key[t * k_st + h * k_sh + u];
+  int64_t blk, off;
+  if constexpr (sizeof(I) == 4) {  // the pool's slots fit 32 bits too
+    const uint32_t b = static_cast<uint32_t>(s) / static_cast<uint32_t>(block_size);
+    blk = b;
+    off = static_cast<uint32_t>(s) - b * static_cast<uint32_t>(block_size);
   } else {
-    v_cache[blk * vc_sb + off * vc_st + h * vc_sh + u] = value[t * v_st + h * v_sh + u];
+    blk = s / block_size;
+    off = s - blk * block_size;
   }
+  if (!kv)
+    k_cache[blk * kc_sb + off * kc_st + h * kc_sh + u] = x;
+  else
+    v_cache[blk * vc_sb + off * vc_st + h * vc_sh + u] = x;
 }
 
 template <typename W, typename SlotT>
@@ -59,17 +69,23 @@ static int launch_append(const void* key, const int64_t* ks, const void* value,
                          int64_t T, int64_t H, int64_t D, int64_t bs,
                          int64_t nblocks, int64_t es, hipStream_t stream) {
   const int64_t f = static_cast<int64_t>(sizeof(W)) / es;  // elements per unit
-  const int32_t upr = static_cast<int32_t>(D / f);
-  const int64_t total = 2 * T * H * upr;
-  const int64_t grid = (total + 255) / 256;
-  hipLaunchKernelGGL((reshape_and_cache_kernel<W, SlotT>), dim3(grid), dim3(256),
-                     0, stream, static_cast<const W*>(key),
-                     static_cast<const W*>(value), static_cast<W*>(kc),
-                     static_cast<W*>(vc), static_cast<const SlotT*>(slots), T,
-                     static_cast<int32_t>(H), upr, ks[0] / f, ks[1] / f,
-                     vs[0] / f, vs[1] / f, kcs[0] / f, kcs[1] / f, kcs[2] / f,
-                     vcs[0] / f, vcs[1] / f, vcs[2] / f,
-                     static_cast<int32_t>(bs), nblocks * bs);
+  const int64_t upr = D / f;
+  const int64_t per_kv = T * H * upr;
+  const int64_t grid = (2 * per_kv + 255) / 256;
+  const W* k = static_cast<const W*>(key);
+  const W* v = static_cast<const W*>(value);
+  const SlotT* sl = static_cast<const SlotT*>(slots);
+  if (2 * per_kv < (int64_t{1} << 31) && nblocks * bs < (int64_t{1} << 31))
+    hipLaunchKernelGGL((reshape_and_cache_kernel<W, SlotT, uint32_t>), dim3(grid), dim3(256), 0, stream, k, v,
+                       static_cast<W*>(kc), static_cast<W*>(vc), sl, static_cast<uint32_t>(per_kv),
+                       static_cast<uint32_t>(H), static_cast<uint32_t>(upr), ks[0] / f, ks[1] / f,
+                       vs[0] / f, vs[1] / f, kcs[0] / f, kcs[1] / f, kcs[2] / f, vcs[0] / f,
+                       vcs[1] / f, vcs[2] / f, static_cast<int32_t>(bs), nblocks * bs);
+  else
+    hipLaunchKernelGGL((reshape_and_cache_kernel<W, SlotT, int64_t>), dim3(grid), dim3(256), 0, stream, k, v,
+                       static_cast<W*>(kc), static_cast<W*>(vc), sl, per_kv, H, upr, ks[0] / f,
+                       ks[1] / f, vs[0] / f, vs[1] / f, kcs[0] / f, kcs[1] / f, kcs[2] / f,
+                       vcs[0] / f, vcs[1] / f, vcs[2] / f, static_cast<int32_t>(bs), nblocks * bs);
   return launch_status("reshape_and_cache");
 }
 
