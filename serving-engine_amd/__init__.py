@@ -3,7 +3,8 @@
 Drop-in for the hot path of the reference engine (ayush-os/serving-engine):
 paged attention, KV append, block copy and step metadata run as hand-written
 gfx950 HIP kernels in libkvhot.so (C ABI: include/kvhot.h), called through
-ctypes.  The directory name is not a Python identifier, so import it with
+ctypes.  BlockManager and Scheduler restate the reference's block pool and
+admission policy on the host, with copy-on-write of shared blocks.  The directory name is not a Python identifier, so import it with
 ``importlib.import_module("serving-engine_amd")``.
 """
 from .block import BLOCK_SIZE
@@ -24,16 +25,21 @@ from .model_runner import (
     step_inputs,
 )
 from .decode_graph import DecodeStepGraph
-from .request import Request, RequestPhase, SchedulerOutput
+from .request import Request, RequestPhase, RequestStatus, SchedulerOutput
+from .block_manager import BlockManager
+from .scheduler import Scheduler
 
 __all__ = [
     "BLOCK_SIZE",
+    "BlockManager",
     "DecodeStepGraph",
     "PAGED_K_TILE_SIZE",
     "PAGED_Q_TILE_SIZE",
     "PAGED_HIP_ATTN_IMPL",
     "Request",
     "RequestPhase",
+    "RequestStatus",
+    "Scheduler",
     "SchedulerOutput",
     "_PagedKVCache",
     "allocate_kv_cache",

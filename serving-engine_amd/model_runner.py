@@ -12,6 +12,7 @@ serving_engine/model_runner.py, running on libkvhot.
   does not import transformers).
 * ``allocate_kv_cache`` / ``num_blocks_for_memory``: the pool of
   serving_engine/model_runner.py:101-125.
+* ``step_inputs``: a step's metadata, after its copy-on-write block copies.
 
 Model loading, tokenisation and sampling stay with the caller.
 """
@@ -165,9 +166,18 @@ def num_blocks_for_memory(free_bytes, num_layers, num_kv_heads, head_dim, dtype=
     return int(free_bytes * gpu_memory_utilization) // per_block
 
 
-def step_inputs(scheduler_output, device="cuda"):
+def step_inputs(scheduler_output, device="cuda", cache=None):
     """Per-step device inputs of ModelRunner.forward's paged path
     (serving_engine/model_runner.py:142-184): the metadata dict, whose
-    ``slot_mapping`` is the write_index and ``positions`` the position ids."""
+    ``slot_mapping`` is the write_index and ``positions`` the position ids.
+    With ``cache``, the step's copy-on-write pairs
+    (scheduler_output.blocks_to_copy, from scheduler.Scheduler) are copied
+    first, on the same stream, so the step's appends land in the copies."""
+    copies = getattr(scheduler_output, "blocks_to_copy", None)
+    if copies:
+        if cache is None:
+            raise ValueError("the step has copy-on-write block copies: pass the cache")
+        src, dst = zip(*copies)
+        cache.copy_blocks(list(src), list(dst))
     meta = build_paged_batch_metadata(scheduler_output, device=device)
     return meta, meta.get("slot_mapping"), meta.get("positions")
