@@ -30,7 +30,10 @@ launch; the eager per-call time, host dispatch included, is reported beside
 it); `traffic` = the HBM bytes rocprofv3's FETCH_SIZE and
 WRITE_SIZE counters read for the same call, scaled by what they read for a
 copy of known size, as recorded in profiles/attention_decode_gqa64_traffic.md
-(null when that file is absent).  cpu_baseline = the reference's eager
+(null when that file is absent).  head_major_pool = the same attention calls
+on a copy of the pool stored block-wise as [Hkv, 16, D]
+(allocate_kv_cache(head_major=True); same shape, values and results; not the
+headline, which keeps the reference's layout).  cpu_baseline = the reference's eager
 PyTorch path (restated in oracle/eager.py) on this host's cores, on one layer
 of the same batch.
 
@@ -64,6 +67,8 @@ def parse():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", type=int, default=2, choices=[2, 3, 4, 5])
+    ap.add_argument("--head-major", action="store_true",
+                    help="pool stored block-wise as [Hkv, block_size, D] (allocate_kv_cache(head_major=True))")
     ap.add_argument("--layers", type=int, default=32)
     ap.add_argument("--partition-tokens", type=int, default=0)
     ap.add_argument("--kernel-reps", type=int, default=10, help="passes over all layers for the kernel timing")
@@ -149,7 +154,7 @@ def main():
 
     w = wl.make_workload(args.workload)
     layers = args.layers if args.workload != 5 else 1  # the 40 GB pool is one layer's
-    t = wl.make_tensors(w, dev, num_layers=layers)
+    t = wl.make_tensors(w, dev, num_layers=layers, head_major=args.head_major)
     cache = sea._PagedKVCache(t.kv_cache)
     meta = sea.build_paged_batch_metadata(w.scheduler_output(), device=dev)
     slots = meta["slot_mapping"]
@@ -221,6 +226,23 @@ def main():
     append_us, append_eager_us = per_launch_us(
         lambda: [cache.write(t.new_k, t.new_v, i, slots) for i in range(layers)])
 
+    # The same calls on a copy of the pool stored block-wise as [Hkv, 16, D]
+    # (allocate_kv_cache(head_major=True)): same shape, values and results.
+    head_major = None
+    if not args.head_major:
+        kv2 = sea.allocate_kv_cache(layers, w.num_blocks, w.num_kv_heads, w.head_dim, dtype=w.dtype,
+                                    device=dev, head_major=True)
+        kv2.copy_(t.kv_cache)
+        blocks2 = [(kv2[i, 0], kv2[i, 1]) for i in range(layers)]
+        hm_us, _ = per_launch_us(lambda: [
+            sea.paged_flash_attention(t.q, blocks2[i][0], blocks2[i][1], meta, w.num_q_heads, w.num_kv_heads,
+                                      scale, partition_tokens=pt) for i in range(layers)])
+        del kv2, blocks2
+        hm_gbs = attn_bytes / (hm_us * 1e-6) / 1e9
+        head_major = {"pool_layout": "head-major blocks [Hkv, 16, D] (allocate_kv_cache(head_major=True))",
+                      "avg_launch_us": round(hm_us, 3), "achieved": round(hm_gbs, 2), "unit": "GB/s",
+                      "frac": round(hm_gbs / HBM_PEAK_GBS, 4)}
+
     prefill = None
     if not args.no_prefill:
         prefill = prefill_measure(sea, wl, dev, reps=max(1, args.kernel_reps // 2))
@@ -259,6 +281,7 @@ def main():
             "append_tokens": w.total_query,
             "partition_tokens": pt or "auto",
             "seed": w.seed,
+            "pool_layout": "head-major blocks [Hkv, 16, D]" if args.head_major else "the reference's [16, Hkv, D] blocks",
         },
         "pct_of_hbm_peak": round(100.0 * value / HBM_PEAK_GBS, 2),
         "roofline": {
@@ -275,6 +298,7 @@ def main():
             "avg_launch_us_timing": "HIP events over replays of one recorded graph of the 32 back-to-back calls",
             "eager_call_us": round(attn_eager_us, 3),
         },
+        "head_major_pool": head_major,
         "append": {"avg_launch_us": round(append_us, 3), "eager_call_us": round(append_eager_us, 3),
                    "algorithmic_bytes": append_bytes,
                    "gbs": round(append_bytes / (append_us * 1e-6) / 1e9, 2)},

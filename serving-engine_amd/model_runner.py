@@ -81,8 +81,9 @@ class _PagedKVCache:
         read tensor (serving_engine/model_runner.py:34-40).  Only the write is
         on the hot path; the gather serves the dense eager attention."""
         self.write(key_states, value_states, layer_idx, write_index)
-        k_cache = self.kv_cache[layer_idx, 0].view(-1, self.num_kv_heads, self.head_dim)
-        v_cache = self.kv_cache[layer_idx, 1].view(-1, self.num_kv_heads, self.head_dim)
+        # reshape: a view for the reference's layout, a copy for a head-major pool
+        k_cache = self.kv_cache[layer_idx, 0].reshape(-1, self.num_kv_heads, self.head_dim)
+        v_cache = self.kv_cache[layer_idx, 1].reshape(-1, self.num_kv_heads, self.head_dim)
         return torch.index_select(k_cache, 0, read_index), torch.index_select(v_cache, 0, read_index)
 
     def blocks(self, layer_idx):
@@ -115,8 +116,8 @@ class _PagedKVCache:
         kv = self.kv_cache
         es = kv.element_size()
         block_bytes = kv[0, 0, 0].numel() * es
-        if not kv[0, 0, 0].is_contiguous():
-            raise ValueError("each block's [block_size, Hkv, D] payload must be contiguous")
+        if not _dense(kv[0, 0, 0]):
+            raise ValueError("each block's [block_size, Hkv, D] payload must fill one dense range")
         lib = _lib.load()
         status = lib.kvhot_copy_blocks(
             kv.data_ptr(), kv.shape[0], kv.stride(0) * es, kv.stride(1) * es,
@@ -151,9 +152,31 @@ def register_attention(name: str = PAGED_HIP_ATTN_IMPL) -> str:
     return name
 
 
+def _dense(t):
+    """Whether t's elements fill one dense range of memory in some order of
+    its dimensions (a block's payload in either pool layout)."""
+    dims = sorted((st, sz) for st, sz in zip(t.stride(), t.shape) if sz > 1)
+    span = 1
+    for st, sz in dims:
+        if st != span:
+            return False
+        span *= sz
+    return True
+
+
 def allocate_kv_cache(num_layers, num_blocks, num_kv_heads, head_dim, dtype=torch.bfloat16,
-                      device="cuda", block_size=BLOCK_SIZE):
-    """Zero-filled pool [L, 2, N, block_size, Hkv, D] (serving_engine/model_runner.py:101-110)."""
+                      device="cuda", block_size=BLOCK_SIZE, head_major=False):
+    """Zero-filled pool [L, 2, N, block_size, Hkv, D] (serving_engine/model_runner.py:101-110).
+
+    head_major=True keeps that shape and indexing but stores each block as
+    [Hkv, block_size, D] (the tensor is a transposed view), so the 16 rows of
+    one kv head in a block are one contiguous 2*16*D-byte range.  Decode reads
+    a block one kv head at a time, and in the reference's token-major order a
+    head's rows sit at a fixed offset inside each token's [Hkv, D] row, which
+    on MI355X maps some heads to slower HBM channels than others."""
+    if head_major:
+        return torch.zeros(num_layers, 2, num_blocks, num_kv_heads, block_size, head_dim,
+                           dtype=dtype, device=device).transpose(3, 4)
     return torch.zeros(num_layers, 2, num_blocks, block_size, num_kv_heads, head_dim,
                        dtype=dtype, device=device)
 

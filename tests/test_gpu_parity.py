@@ -268,6 +268,35 @@ def test_config3_mixed_prefill_decode(cuda, sea, wl):
     assert_attention(w, o, l, ref_o, ref_l)
 
 
+@pytest.mark.parametrize("config", [2, 3])
+def test_head_major_pool(cuda, sea, wl, config):
+    """The pool stored block-wise as [Hkv, 16, D] (allocate_kv_cache(head_major=True)):
+    same shape and values, other strides; append, attention and block copy
+    give what they give on the reference's layout."""
+    w = wl.make_workload(config)
+    announce(f"attention workload {config} on a head-major pool")
+    T = wl.make_tensors(w, cuda, head_major=True)
+    assert T.kv_cache.stride()[3:] == (w.head_dim, 16 * w.head_dim, 1)
+    ref_o, ref_l = oracle_step(w, T)
+    meta = sea.build_paged_batch_metadata(w.scheduler_output(), device=cuda) if config == 3 else None
+    o, l = hip_step(sea, wl, w, T, meta=meta)
+    assert_attention(w, o, l, ref_o, ref_l)
+    # the append landed in the head-major slots bit-exactly
+    slots = T.slot_mapping.cpu()
+    kc = T.kv_cache[0, 0].reshape(-1, w.num_kv_heads, w.head_dim)
+    assert torch.equal(kc[slots.to(cuda)].cpu(), T.new_k.transpose(1, 2).squeeze(0).cpu())
+    # block copy moves whole head-major blocks
+    cache = sea._PagedKVCache(T.kv_cache)
+    before = T.kv_cache.clone()
+    src = int(slots[0]) // 16
+    dst = w.num_blocks - 1 if src != w.num_blocks - 1 else w.num_blocks - 2
+    cache.copy_blocks([src], [dst])
+    torch.cuda.synchronize()
+    assert torch.equal(T.kv_cache[:, :, dst], before[:, :, src])
+    rest = torch.arange(w.num_blocks, device=cuda) != dst
+    assert torch.equal(T.kv_cache[:, :, rest], before[:, :, rest])
+
+
 def test_config4_prefix_sharing_and_cow(cuda, sea, wl):
     w = wl.make_workload(4)
     announce("attention workload 4 (256 rows sharing 64 blocks) + copy-on-write")
