@@ -263,7 +263,7 @@ def test_randomized_run_keeps_the_pool_consistent():
                 r.output_token_ids.append(rng.randint(0, 99))
         s.update_after_step(out)
         held = {}
-        for r in s.running:
+        for r in s.running + s.waiting:  # a waiting request may hold prefix-matched blocks
             for b in r.block_table:
                 held[b] = held.get(b, 0) + 1
         bm = s.block_manager
@@ -271,4 +271,51 @@ def test_randomized_run_keeps_the_pool_consistent():
         assert sorted(bm.free_blocks) == [b for b in range(nblocks) if b not in held]
         steps += 1
         assert steps < 2000
+    assert s.block_manager.get_num_free_blocks() == nblocks
+
+
+def test_randomized_run_with_forks_keeps_copies_and_accounting_consistent():
+    rng = random.Random(11)
+    bs, nblocks = 4, 40
+    s = sched(nblocks, bs=bs, max_num_batched_tokens=20, max_num_seqs=8, min_chunk_size=2)
+    pending = [req(f"r{i}", rng.randint(2, 18), max_new=rng.randint(2, 10)) for i in range(24)]
+    nfork = copies = 0
+    for step in range(3000):
+        if not pending and not s.has_unfinished_requests():
+            break
+        if pending and rng.random() < 0.4:
+            s.add_request(pending.pop())
+        decoding = [r for r in s.running if r.phase == RequestPhase.NEEDS_DECODE and r.block_table]
+        if decoding and rng.random() < 0.3 and s.block_manager.get_num_free_blocks() > 2:
+            p = rng.choice(decoding)
+            c = Request(request_id=f"f{nfork}", prompt_token_ids=list(p.prompt_token_ids),
+                        output_token_ids=list(p.output_token_ids), max_new_tokens=p.max_new_tokens)
+            c.num_computed_tokens, c.phase, c.status = p.num_computed_tokens, p.phase, RequestStatus.RUNNING
+            s.block_manager.fork(p, c)
+            s.running.append(c)
+            nfork += 1
+        held_before = {b for r in s.running + s.waiting for b in r.block_table}
+        free_before = set(s.block_manager.free_blocks)
+        out = s.schedule()
+        for src, dst in out.blocks_to_copy:
+            assert src in held_before and dst in free_before and src != dst
+            assert any(dst in r.block_table for r in out.scheduled_requests)
+        assert len({d for _, d in out.blocks_to_copy}) == len(out.blocks_to_copy)
+        copies += len(out.blocks_to_copy)
+        for r in out.scheduled_requests:
+            if r.phase == RequestPhase.NEEDS_DECODE:
+                i = (r.total_len - 1) // bs  # the block this step writes is this row's alone
+                assert s.block_manager.blocks[r.block_table[i]].ref_count == 1
+            if r.phase == RequestPhase.NEEDS_DECODE or r.request_id in out.prefill_final_chunk:
+                r.output_token_ids.append(rng.randint(0, 99))
+        s.update_after_step(out)
+        held = {}
+        for r in s.running + s.waiting:  # a waiting request may hold prefix-matched blocks
+            for b in r.block_table:
+                held[b] = held.get(b, 0) + 1
+        bm = s.block_manager
+        assert all(bm.blocks[b].ref_count == held.get(b, 0) for b in range(nblocks))
+        assert sorted(bm.free_blocks) == [b for b in range(nblocks) if b not in held]
+    assert not pending and not s.has_unfinished_requests()
+    assert nfork > 0 and copies > 0
     assert s.block_manager.get_num_free_blocks() == nblocks
