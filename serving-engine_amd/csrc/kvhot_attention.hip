@@ -920,15 +920,41 @@ attn_merge_kernel(const AttnArgs a) {
         }
       }
     } else {
-      for (int pp = 0; pp < nparts; ++pp) mmax = fmaxf(mmax, a.ws_lse[(base + pp) * G + hh]);
-      if (mmax != -INFINITY) {
-        for (int pp = 0; pp < nparts; ++pp) {
-          const float w = fast_exp2(a.ws_lse[(base + pp) * G + hh] - mmax);
-          lsum += w;
-          const f32x4* src = reinterpret_cast<const f32x4*>(a.ws_o + ((base + pp) * G + hh) * D + 8 * c);
-          acc0 += w * src[0];
-          acc1 += w * src[1];
+      // One pass, kBatch parts at a time: a batch's loads are issued
+      // together, then folded in with the running max moved (long rows have
+      // tens of parts, and a part-by-part loop waits for each load in turn).
+      constexpr int kBatch = 8;
+      for (int b0 = 0; b0 < nparts; b0 += kBatch) {
+        float lv[kBatch];
+        f32x4 p0[kBatch], p1[kBatch];
+#pragma unroll
+        for (int k = 0; k < kBatch; ++k) {
+          lv[k] = -INFINITY;
+          p0[k] = p1[k] = f32x4{0.f, 0.f, 0.f, 0.f};
+          if (b0 + k < nparts) {
+            lv[k] = a.ws_lse[(base + b0 + k) * G + hh];
+            const f32x4* src = reinterpret_cast<const f32x4*>(a.ws_o + ((base + b0 + k) * G + hh) * D + 8 * c);
+            p0[k] = src[0];
+            p1[k] = src[1];
+          }
         }
+        float bmax = -INFINITY;
+#pragma unroll
+        for (int k = 0; k < kBatch; ++k) bmax = fmaxf(bmax, lv[k]);
+        if (bmax == -INFINITY) continue;
+        const float mnew = fmaxf(mmax, bmax);
+        const float corr = fast_exp2(mmax - mnew);  // 0 while mmax is -inf
+        lsum *= corr;
+        acc0 *= corr;
+        acc1 *= corr;
+#pragma unroll
+        for (int k = 0; k < kBatch; ++k) {
+          const float w = fast_exp2(lv[k] - mnew);
+          lsum += w;
+          acc0 += w * p0[k];
+          acc1 += w * p1[k];
+        }
+        mmax = mnew;
       }
     }
     const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
