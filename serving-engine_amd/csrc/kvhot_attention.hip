@@ -851,15 +851,20 @@ attn_decode_kernel(const AttnArgs a) {
 // Combines the parts of split decode segments: (row, kv head) pieces that
 // ran in different work-groups and left (LSE, O) partials.  With a schedule,
 // work-group u takes merge unit u = (query token, kv head, parts, first
-// partial index), each lane 8 head_dim values of one of the G query heads.
-// Without one, the grid is (head_dim chunks, rows), and a row's parts are the
-// fixed partitions of part_tokens keys, recomputed as the decode kernel did.
+// partial index), each lane 8 head_dim values of one of the G query heads;
+// the kMergeWaves waves of the work-group fold a share of the parts each and
+// combine their states through LDS.  Without one, the grid is (head_dim
+// chunks, rows) of one-wave work-groups, and a row's parts are the fixed
+// partitions of part_tokens keys, recomputed as the decode kernel did.
+constexpr int kMergeWaves = 4;
+
 template <class TT, int D>
-__global__ void __launch_bounds__(64)
+__global__ void __launch_bounds__(64 * kMergeWaves)
 attn_merge_kernel(const AttnArgs a) {
   using st = uint16_t;
   constexpr int CH = D / 8;
   const int G = a.G;
+  const int wv = static_cast<int>(threadIdx.x >> 6), nwv = static_cast<int>(blockDim.x >> 6);
   int64_t t, base;
   int kvh, nparts, it0, step;
   if (a.merge_units) {
@@ -868,7 +873,7 @@ attn_merge_kernel(const AttnArgs a) {
     kvh = u.y;
     nparts = u.z;
     base = u.w;
-    it0 = threadIdx.x;
+    it0 = threadIdx.x & 63;
     step = 64;
   } else {
     const int row = blockIdx.y;
@@ -888,6 +893,8 @@ attn_merge_kernel(const AttnArgs a) {
       base + nparts > a.num_partials)
     return;
   constexpr int kFew = 4;  // up to this many parts, every load is issued at once
+  if (nparts <= kFew && wv > 0) return;  // one wave folds a few parts
+  __shared__ float part_state[kMergeWaves][64][10];  // max, sum, O (8 values) per wave and lane
   for (int it = it0; it < G * CH; it += step) {
     const int hh = it / CH;
     const int c = it % CH;
@@ -924,14 +931,16 @@ attn_merge_kernel(const AttnArgs a) {
       // together, then folded in with the running max moved (long rows have
       // tens of parts, and a part-by-part loop waits for each load in turn).
       constexpr int kBatch = 8;
-      for (int b0 = 0; b0 < nparts; b0 += kBatch) {
+      const int lo = static_cast<int>((static_cast<int64_t>(nparts) * wv) / nwv);
+      const int hi = static_cast<int>((static_cast<int64_t>(nparts) * (wv + 1)) / nwv);
+      for (int b0 = lo; b0 < hi; b0 += kBatch) {
         float lv[kBatch];
         f32x4 p0[kBatch], p1[kBatch];
 #pragma unroll
         for (int k = 0; k < kBatch; ++k) {
           lv[k] = -INFINITY;
           p0[k] = p1[k] = f32x4{0.f, 0.f, 0.f, 0.f};
-          if (b0 + k < nparts) {
+          if (b0 + k < hi) {
             lv[k] = a.ws_lse[(base + b0 + k) * G + hh];
             const f32x4* src = reinterpret_cast<const f32x4*>(a.ws_o + ((base + b0 + k) * G + hh) * D + 8 * c);
             p0[k] = src[0];
@@ -955,6 +964,33 @@ attn_merge_kernel(const AttnArgs a) {
           acc1 += w * p1[k];
         }
         mmax = mnew;
+      }
+      if (nwv > 1) {
+        // The waves' states meet in LDS; wave 0 combines them.
+        float* my = part_state[wv][threadIdx.x & 63];
+        my[0] = mmax;
+        my[1] = lsum;
+        my[2] = acc0.x; my[3] = acc0.y; my[4] = acc0.z; my[5] = acc0.w;
+        my[6] = acc1.x; my[7] = acc1.y; my[8] = acc1.z; my[9] = acc1.w;
+        __syncthreads();
+        if (wv == 0) {
+          float m2 = -INFINITY;
+          for (int w = 0; w < nwv; ++w) m2 = fmaxf(m2, part_state[w][threadIdx.x][0]);
+          lsum = 0.f;
+          acc0 = acc1 = f32x4{0.f, 0.f, 0.f, 0.f};
+          if (m2 != -INFINITY) {
+            for (int w = 0; w < nwv; ++w) {
+              const float* q = part_state[w][threadIdx.x];
+              const float c2 = fast_exp2(q[0] - m2);  // 0 for a wave that saw no part
+              lsum += c2 * q[1];
+              acc0 += c2 * f32x4{q[2], q[3], q[4], q[5]};
+              acc1 += c2 * f32x4{q[6], q[7], q[8], q[9]};
+            }
+          }
+          mmax = m2;
+        }
+        __syncthreads();  // the states are read before the next item writes them
+        if (wv > 0) continue;
       }
     }
     const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
@@ -1784,7 +1820,7 @@ static void launch_mfma(const AttnArgs& a, int waves, int64_t rows, int64_t max_
     if (a.sched ? n_merge > 0 : a.max_parts > 1) {
       dim3 mgrid = a.sched ? dim3(static_cast<uint32_t>(n_merge))
                            : dim3(static_cast<uint32_t>((a.Hq * (D / 8) + 63) / 64), static_cast<uint32_t>(rows));
-      hipLaunchKernelGGL((attn_merge_kernel<TT, D>), mgrid, dim3(64), 0, stream, a);
+      hipLaunchKernelGGL((attn_merge_kernel<TT, D>), mgrid, dim3(a.sched ? 64 * kMergeWaves : 64), 0, stream, a);
     }
   }
   if (aux) {
