@@ -308,7 +308,7 @@ def test_config4_prefix_sharing_and_cow(cuda, sea, wl):
     cache = sea._PagedKVCache(T.kv_cache)
     cache.copy_blocks(w.copy_src, w.copy_dst)
     meta = wl.metadata_tensors(w, cuda)
-    bt, host_bt = meta["block_table"], meta["host_block_table"]  # the schedule reads the host copy
+    bt, host_bt = meta["block_table"], meta["host_block_table"]  # host copy kept equal to the device table
     for i, x in enumerate(w.rows):
         bt[i, math.ceil(x.k_len / 16) - 1] = int(w.copy_dst[i])
         host_bt[i, math.ceil(x.k_len / 16) - 1] = int(w.copy_dst[i])
