@@ -119,72 +119,50 @@ int kvhot_build_slot_mapping(const int32_t* block_table, int64_t bt_row_stride,
                              int64_t* positions, void* stream);
 
 /*
- * Every workspace starts with this many bytes of counters used by scheduled
- * decode calls (rows whose keys were cut across work-groups).  They must be
- * zero before a workspace's first call, and every call leaves them zero, so
- * allocate workspaces zero-filled.  Split-K partials follow them.
- */
-#define KVHOT_WORKSPACE_COUNTER_BYTES 16384
-
-/*
  * Workspace bytes kvhot_paged_attention needs for these sizes when it is
- * called WITHOUT a schedule (0 if it needs none): the counter bytes above,
- * then split-K partition results of decode rows, fully rewritten by each call
- * before they are read.  A workspace may be reused by calls of any shape that
- * fits.  Calls sharing a workspace must be ordered on one stream.  Returns a
- * negative KVHOT_E* code for invalid sizes.  (With a schedule, the size comes
- * from kvhot_paged_attention_schedule.)
+ * called WITHOUT a schedule (0 if it needs none): split-K partition results
+ * of decode rows, fully rewritten by each call before they are read, so a
+ * workspace needs no initialisation and may be reused by calls of any shape
+ * that fits.  Calls sharing a workspace must be ordered on one stream.
+ * Returns a negative KVHOT_E* code for invalid sizes.  (With a schedule, the
+ * size comes from kvhot_paged_attention_schedule.)
  */
 int64_t kvhot_paged_attention_workspace_bytes(
     int64_t num_rows, int64_t total_query, int64_t max_q_len,
     int64_t max_k_len, int64_t num_q_heads, int64_t num_kv_heads,
     int64_t head_dim, int64_t block_size, int64_t partition_tokens, int dtype);
 
-/* Entries of the description kvhot_paged_attention_schedule writes beside a
- * launch list; kvhot_paged_attention takes it back unchanged. */
-enum {
-  KVHOT_SCHED_UNITS = 0,           /* units in the list (8 int32 each) */
-  KVHOT_SCHED_PREFILL_UNITS = 1,   /* prefill work-groups: units [0, n) */
-  KVHOT_SCHED_DECODE_UNITS = 2,    /* the decode section: the n units after them */
-  KVHOT_SCHED_DECODE_GROUPS = 3,   /* work-groups of the decode launch */
-  KVHOT_SCHED_WORKSPACE_BYTES = 4, /* workspace the attention call needs (0: none) */
-  KVHOT_SCHED_CUT_ROWS = 5,        /* decode rows whose keys are cut across work-groups */
-  KVHOT_SCHED_DECODE_LDS_BYTES = 6,/* LDS of a decode work-group */
-  KVHOT_SCHED_DECODE_BANKS = 7,    /* its per-piece accumulators (| 256: one slot per wave) */
-  KVHOT_SCHED_INFO_LEN = 8
-};
-
 /*
  * Launch list ("schedule") for kvhot_paged_attention, built on the host from
- * HOST copies of q_lens, k_lens, q_starts and q_pos_offsets, with the head
- * counts, head_dim, block_size, is_causal and dtype the attention call will
- * get.  Units of 8 int32: the prefill work-groups (row, kv head, query block;
- * longest key range first), then the decode section.  Decode rows run as
- * head groups: the 16-token slices of all decode rows, rows in order, are cut
- * into equal ranges, one per group of num_kv_heads work-groups, and work-group
- * q * num_kv_heads + i streams kv head (i + q) % num_kv_heads of range q, so a
- * group's work-groups read every block of the range at about the same time.  A row cut between
- * two ranges is combined inside the launch by whichever of its pieces
- * finishes last (through the workspace).  partition_tokens > 0 (a multiple of
- * 32 up to 2^20) makes every such cut fall on a multiple of that many keys
- * into the row; 0 lets the planner cut anywhere (at least 64 keys from
- * either end of a piece).  info (KVHOT_SCHED_INFO_LEN entries) receives the
- * unit counts, the decode launch's work-groups and the workspace the
- * attention call needs.  Returns the total unit count (units are written when
- * `units` is non-NULL and capacity_units suffices) or a negative KVHOT_E*
- * code; 0 units means no schedule (shapes the MFMA kernels do not take, or
- * counts beyond the list's fields): call kvhot_paged_attention without one.
- * A schedule depends only on the step's lengths, so one upload serves every
- * layer of an engine step.  Without a schedule the attention launch covers
- * the padded grid of (row, partition, head group), and work-groups without
- * work still cost a launch slot each.
+ * HOST copies of q_lens, k_lens, q_starts, q_pos_offsets and the block table,
+ * with the head counts, head_dim, block_size, is_causal and dtype the
+ * attention call will get.  The (row, kv head) key ranges of decode rows are
+ * laid end to end and cut into equal numbers of 16-token slices per decode
+ * work-group, one device-full of work-groups; a range cut in two becomes
+ * "parts" in different work-groups.  Units of 8 int32, in order:
+ * num_decode_units per-wave descriptors (whole work-groups; each carries its
+ * row's metadata and first block, so the wave's first K/V loads depend on
+ * nothing else), num_prefill_units per-work-group prefill units (longest
+ * first), num_merge_units units, one per decode range cut into parts.
+ * partition_tokens > 0 (a multiple of 32 up to 2^20) first cuts every decode
+ * row into partitions of that many keys, which are then never cut further;
+ * 0 leaves the cuts to the planner.  *workspace_bytes receives the workspace
+ * the attention call needs with this schedule (0: none).  Returns the total
+ * unit count (units are written when `units` is non-NULL and capacity_units
+ * suffices) or a negative KVHOT_E* code.  A schedule depends only on the
+ * step's lengths, so one upload serves every layer of an engine step.
+ * Without a schedule the attention launch covers the padded grid of (row,
+ * partition, head group), and work-groups without work still cost a launch
+ * slot each.
  */
 int64_t kvhot_paged_attention_schedule(
     const int32_t* q_lens, const int32_t* k_lens, const int32_t* q_starts,
-    const int32_t* q_pos_offsets, int64_t num_rows, int64_t num_q_heads,
-    int64_t num_kv_heads, int64_t head_dim, int64_t block_size,
-    int64_t partition_tokens, int is_causal, int dtype, int32_t* units,
-    int64_t capacity_units, int64_t info[KVHOT_SCHED_INFO_LEN]);
+    const int32_t* q_pos_offsets, const int32_t* block_table,
+    int64_t bt_row_stride, int64_t num_rows, int64_t num_q_heads, int64_t num_kv_heads,
+    int64_t head_dim, int64_t block_size, int64_t partition_tokens,
+    int is_causal, int dtype, int32_t* units, int64_t capacity_units,
+    int64_t* num_decode_units, int64_t* num_prefill_units,
+    int64_t* num_merge_units, int64_t* workspace_bytes);
 
 /*
  * Paged attention forward over a ragged batch of rows (prefill chunks and
@@ -196,22 +174,22 @@ int64_t kvhot_paged_attention_schedule(
  *   out[t, h, :] = softmax_j(scale * q[t,h,:] . k_j) @ v_j   (fp32 accumulate)
  *   lse[t, h]    = natural-log logsumexp_j(scale * q[t,h,:] . k_j)
  * A query with no visible key gets out = 0 and lse = -inf.
- * Rows with n_q == 1 run the flash-decoding kernel, rows with n_q >= 2 the
- * chunked-prefill kernel.  max_q_len / max_k_len must bound q_lens / k_lens
- * (they size the grid; no device->host sync is made).
+ * Rows with n_q == 1 run the split-K flash-decoding kernel, plus a merge
+ * launch when a decode row was split across work-groups; rows with
+ * n_q >= 2 run the chunked-prefill kernel.  max_q_len / max_k_len must bound
+ * q_lens / k_lens (they size the grid; no device->host sync is made).
  * schedule: device copy of the units from kvhot_paged_attention_schedule for
- * exactly these lengths and sizes, schedule_info its description (host
- * memory), and a workspace of at least its KVHOT_SCHED_WORKSPACE_BYTES (a
- * shorter one fails with KVHOT_EWORKSPACE before any launch); or NULL, and
- * then partition_tokens (keys per decode partition; 0 picks a size,
- * otherwise a multiple of 32 up to 2^20) and
- * kvhot_paged_attention_workspace_bytes apply (plus a merge launch for rows
- * of several partitions).  With a schedule, the waves of a work-group claim
- * slices at run time, so the summation order, and with it the last bits of
- * out and lse, can differ from call to call.  lse may be NULL.  out has the
- * dtype of q, k_cache and v_cache; lse is fp32.  Replaces
- * paged_flash_attention + paged_flash_fwd_kernel
- * (serving_engine/paged_attention_kernel.py:16-160).
+ * exactly these lengths and sizes, with its three unit counts, the workspace
+ * size it reported (schedule_workspace_bytes) and a workspace at least that
+ * large (a shorter one fails with KVHOT_EWORKSPACE before any launch); or
+ * NULL, and then partition_tokens (keys per
+ * decode partition; 0 picks a size, otherwise a multiple of 32 up to 2^20)
+ * and kvhot_paged_attention_workspace_bytes apply.  With a schedule, decode
+ * waves of one work-group share out their slices at run time, so the
+ * summation order, and with it the last bits of out and lse, can differ from
+ * call to call.  lse may be NULL.  out has the dtype of q, k_cache and
+ * v_cache; lse is fp32.  Replaces paged_flash_attention +
+ * paged_flash_fwd_kernel (serving_engine/paged_attention_kernel.py:16-160).
  */
 int kvhot_paged_attention(
     const void* q, const int64_t q_strides[3],
@@ -226,7 +204,9 @@ int kvhot_paged_attention(
     int64_t num_kv_heads, int64_t head_dim, int64_t block_size,
     int64_t num_blocks, float scale, int is_causal, int dtype,
     int64_t partition_tokens, const int32_t* schedule,
-    const int64_t* schedule_info, void* workspace, int64_t workspace_bytes,
+    int64_t num_decode_units, int64_t num_prefill_units,
+    int64_t num_merge_units, int64_t schedule_workspace_bytes,
+    void* workspace, int64_t workspace_bytes,
     void* stream);
 
 #ifdef __cplusplus

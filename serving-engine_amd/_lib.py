@@ -57,24 +57,17 @@ SIGNATURES = {
     ),
     "kvhot_paged_attention_schedule": (
         _i64,
-        [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _int, _int, _vp, _i64, _i64p],
+        [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _int, _int, _vp, _i64,
+         _i64p, _i64p, _i64p, _i64p],
     ),
     "kvhot_paged_attention": (
         _int,
         [_vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p,
          _vp, _i64, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64,
-         _i64, _i64, _i64, _i64, ctypes.c_float, _int, _int, _i64, _vp, _i64p,
+         _i64, _i64, _i64, _i64, ctypes.c_float, _int, _int, _i64, _vp, _i64, _i64, _i64, _i64,
          _vp, _i64, _vp],
     ),
 }
-
-# include/kvhot.h: bytes of counters at the start of every workspace (zero
-# before its first use; every call leaves them zero), and the entries of a
-# schedule's description.
-WORKSPACE_COUNTER_BYTES = 16384
-SCHED_UNITS, SCHED_PREFILL_UNITS, SCHED_DECODE_UNITS, SCHED_DECODE_GROUPS, SCHED_WORKSPACE_BYTES, \
-    SCHED_CUT_ROWS, SCHED_DECODE_LDS_BYTES, SCHED_DECODE_BANKS = range(8)
-SCHED_INFO_LEN = 8
 
 
 class KvhotError(RuntimeError):

@@ -76,13 +76,8 @@ struct AttnArgs {
   // prefill: two int4 per work-group), or null: then the grid enumerates every
   // (row, partition, head group) and work-groups without work exit.
   const int4* sched;
-  int32_t dec_slots;  // LDS (LSE, O) slots of a grid-mode decode work-group, >= its waves
-  // Scheduled decode: the launch list's decode section, the cut-row counters
-  // (zero between calls) and the LDS accumulator banks per work-group.
-  const int4* dsched;
-  int* merge_ctr;
-  int32_t dec_banks;
-  int32_t dec_slot_mode;  // 1: per-wave slots in each bank, 0: a locked shared accumulator
+  const int4* merge_units;  // schedule: two int4 per split decode segment
+  int32_t dec_slots;  // LDS (LSE, O) slots of a decode work-group, >= its waves
 };
 
 __device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
@@ -114,11 +109,6 @@ __device__ inline const T* uniform_ptr(const T* p) {
 __device__ inline __amdgpu_buffer_rsrc_t block_rsrc(const void* base, int bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, 0x00020000);
 }
-
-// Cache-policy bit of buffer loads and stores for device (agent) scope on
-// gfx950: stores write through to the device-coherent level, loads do not hit
-// in a non-coherent cache (the bits an agent-scope atomic store or load gets).
-constexpr int kSc1 = 16;
 
 // Loads N dwords (N in {2, 4, 8}) at byte offset off (+ uniform soff) of r.
 template <int N>
@@ -258,28 +248,6 @@ struct WaveAttn {
       buffer_dwords<VW>(vr, 2 * ((4 * g + j) * static_cast<int>(a.v_st) + EPL * n), vs, T.v[j]);
   }
 
-  // load_slice_from with the descriptors' range cut to zero when `live` is 0:
-  // the same instructions issue, but they return zeros and touch no memory.
-  // The bases, offset and ranges are broadcast here, at their use: values
-  // that reach a buffer descriptor through a join are otherwise kept per lane,
-  // and every load is wrapped in a loop over distinct descriptors.
-  __device__ void load_slice_bounded(const AttnArgs& a, const st* kb, const st* vb, int bo, int live,
-                                     KVSlice<D>& T) const {
-    const int k_lane = 2 * (n * static_cast<int>(a.k_st) + 8 * g);
-    const int kbytes = __builtin_amdgcn_readfirstlane(live ? static_cast<int>(2 * a.k_sb) : 0);
-    const int vbytes = __builtin_amdgcn_readfirstlane(live ? static_cast<int>(2 * a.v_sb) : 0);
-    const __amdgpu_buffer_rsrc_t kr = block_rsrc(uniform_ptr(kb), kbytes);
-    const __amdgpu_buffer_rsrc_t vr = block_rsrc(uniform_ptr(vb), vbytes);
-    const int ks = __builtin_amdgcn_readfirstlane(2 * bo * static_cast<int>(a.k_st));
-    const int vs = __builtin_amdgcn_readfirstlane(2 * bo * static_cast<int>(a.v_st));
-#pragma unroll
-    for (int c = 0; c < NC; ++c)
-      T.k[c] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(kr, k_lane + 64 * c, ks, 0));
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-      buffer_dwords<VW>(vr, 2 * ((4 * g + j) * static_cast<int>(a.v_st) + EPL * n), vs, T.v[j]);
-  }
-
   // Folds the slice of keys ts..ts+15 into the online softmax.  Keys at or
   // past kstop, and keys past an m-row's causal limit, are masked; qpos_min is
   // the smallest causal limit of the valid m-rows (keys up to it are visible
@@ -344,59 +312,6 @@ struct WaveAttn {
                         __builtin_amdgcn_perm(T.v[3][w], T.v[2][w], sel)};
 #pragma unroll
       for (int s = 0; s < NM; ++s) o[s][e] = TT::mfma16(vt, pb[s], o[s][e]);
-    }
-  }
-
-  // compute_slice with a lazy softmax reference (decode, NM = 1, no causal
-  // limit beyond kstop): m[0] is a reference that only moves when some score
-  // of the slice exceeds it by more than kLazyRescale (then to the exact
-  // running max, with O and l rescaled), so P = 2^(x - m) < 2^kLazyRescale
-  // and most slices need no cross-lane reduction.  m[0] must start finite
-  // (-FLT_MAX): masked keys then give P = 0.
-  __device__ void compute_slice_lazy(const AttnArgs& a, int ts, int kstop, KVSlice<D>& T) {
-    static_assert(NM == 1, "decode only");
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int c = 0; c < NC; ++c) acc = TT::mfma(T.k[c], qf[0][c], acc);
-    const bool tail = ts + 16 > kstop;
-    float x[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      x[j] = acc[j] * a.scale_log2;
-      if (tail) x[j] = ts + 4 * g + j < kstop ? x[j] : -INFINITY;
-    }
-    if (tail) {
-      // Keys past the end may hold any bit pattern; zero them so 0 * V stays 0.
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const bool ok = ts + 4 * g + j < kstop;
-#pragma unroll
-        for (int w = 0; w < VW; ++w) T.v[j][w] = ok ? T.v[j][w] : 0u;
-      }
-    }
-    const float mloc = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
-    if (__builtin_amdgcn_ballot_w64(mloc > m[0] + kLazyRescale) != 0) {
-      float mx = fmaxf(mloc, __shfl_xor(mloc, 16, kWave));
-      mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
-      const float mnew = fmaxf(m[0], mx);
-      const float corr = fast_exp2(m[0] - mnew);
-      m[0] = mnew;
-      l[0] *= corr;
-#pragma unroll
-      for (int e = 0; e < EPL; ++e) o[0][e] *= corr;
-    }
-    float pr[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) pr[j] = fast_exp2(x[j] - m[0]);
-    l[0] += (pr[0] + pr[1]) + (pr[2] + pr[3]);
-    const u32x2 pb = {TT::pack2(pr[0], pr[1]), TT::pack2(pr[2], pr[3])};
-#pragma unroll
-    for (int e = 0; e < EPL; ++e) {
-      const int w = e >> 1;
-      const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
-      const u32x2 vt = {__builtin_amdgcn_perm(T.v[1][w], T.v[0][w], sel),
-                        __builtin_amdgcn_perm(T.v[3][w], T.v[2][w], sel)};
-      o[0][e] = TT::mfma16(vt, pb, o[0][e]);
     }
   }
 
@@ -625,24 +540,28 @@ struct WaveAttn {
   }
 };
 
-// --------------------------------------------------------- decode (grid) --
-// Without a launch list (the caller has no host copies of the lengths), the
-// grid enumerates (head group, partition, row): a decode row's keys are cut
-// into partitions of part_tokens keys, and work-group (group, partition, row)
-// takes W/S kv heads of it, S waves each (S from decode_splits), each wave a
-// range of 16-token slices.
+// --------------------------------------------------------------- decode --
+// A decode row's keys are cut into (row, kv head, partition) segments, and a
+// segment into "ranges" of 16-token slices, one range per wave of a
+// work-group (host schedule from kvhot_paged_attention_schedule, or the grid:
+// work-group (group, partition, row) takes W/S kv heads of one row, S waves
+// each, S from decode_splits).
 //
-// Waves of one CU stream at very different rates, so ranges are only a
-// starting point.  Each wave claims its slices one at a time from an LDS
-// counter; when its range is used up it claims slices from the range with the
-// most left, first among waves of its own segment (the online softmax takes
-// keys in any order), then from other segments.  Every (wave, segment) pair a
-// wave worked on leaves a normalised (LSE, O) in an LDS slot: its own slot
-// first, then slots from a pool of `dec_slots - W` (when the pool is empty
-// the wave stops taking new segments).  After a barrier the first wave of
-// each segment merges that segment's slots.  A row of several partitions
-// stores an (LSE, O) partial per partition to HBM instead, and
-// attn_merge_kernel combines them in a second launch.
+// Waves of one CU stream at very different rates (measured: equal ranges end
+// up to 20 us apart inside one work-group, while work-group means agree to a
+// few percent), so ranges are only a starting point.  Each wave claims its
+// slices one at a time from an LDS counter; when its range is used up it
+// claims slices from the range with the most left, first among waves of its
+// own segment (the online softmax takes keys in any order), then from other
+// segments.  Every (wave, segment) pair a wave worked on leaves a normalised
+// (LSE, O) in an LDS slot: its own slot first, then slots from a pool of
+// `dec_slots - W` (when the pool is empty the wave stops taking new segments).
+// After a barrier the first wave of each segment merges that segment's slots.
+// A segment that is one of several partitions of its row stores an (LSE, O)
+// partial to HBM instead, and attn_merge_kernel combines the partitions in a
+// second launch.  (Merging across work-groups inside one launch needs a
+// device-scope release per wave, which on gfx950 is an L2 write-back per wave
+// -- far slower than a launch.)
 
 #ifndef KVHOT_SLICES_PER_WAVE
 #define KVHOT_SLICES_PER_WAVE 8
@@ -688,11 +607,29 @@ attn_decode_kernel(const AttnArgs a) {
   const int S = a.dec_slots;
 
   // ---- this wave's range: slices [s0, s1) of part `part` of (row, kvh) ----
-  // The grid enumerates (head group, partition, row); work-groups without
-  // work exit.
   int row = -1, kvh = 0, s0 = 0, s1 = 0, part = 0, nparts = 0, kend = 0;
   int64_t qs = 0, pidx = 0;
-  {
+  int d_first = -1;
+  if (a.sched) {
+    // (row | parts << 16, kvh | part << 16, s0, s1), (query token, visible
+    // keys, physical block of slice s0 or -1, partial index)
+    const int4* u = a.sched + 2 * (static_cast<int64_t>(blockIdx.x) * W + wave);
+    const int4 u0 = u[0], u1 = u[1];
+    const int x = __builtin_amdgcn_readfirstlane(u0.x);
+    const int y = __builtin_amdgcn_readfirstlane(u0.y);
+    if (x >= 0) {
+      row = x & 0xffff;
+      nparts = (x >> 16) & 0xffff;
+      kvh = y & 0xffff;
+      part = (y >> 16) & 0xffff;
+    }
+    s0 = __builtin_amdgcn_readfirstlane(u0.z);
+    s1 = __builtin_amdgcn_readfirstlane(u0.w);
+    qs = __builtin_amdgcn_readfirstlane(u1.x);
+    kend = __builtin_amdgcn_readfirstlane(u1.y);
+    d_first = __builtin_amdgcn_readfirstlane(u1.z);
+    pidx = __builtin_amdgcn_readfirstlane(u1.w);
+  } else {
     const int r = blockIdx.z;
     const int p = blockIdx.y;
     if (a.q_lens[r] != 1) return;
@@ -753,7 +690,9 @@ attn_decode_kernel(const AttnArgs a) {
   KVSlice<D> T;
   int i = s0;              // slice whose loads are in flight, if `have`
   bool have = nsl > 0;     // the first slice of the range is taken without a claim
-  if (have) wa.load_slice(a, kvh, block_of(row, s0), kb % bs, T);
+  if (have)
+    wa.load_slice(a, kvh, d_first >= 0 ? min(static_cast<int64_t>(d_first), a.num_blocks - 1) : block_of(row, s0),
+                  kb % bs, T);
   if (lane == 0) {
     cnt[wave] = s0 + (have ? 1 : 0);
     dend[wave] = s0 + nsl;
@@ -909,547 +848,14 @@ attn_decode_kernel(const AttnArgs a) {
   }
 }
 
-// ------------------------------------------------------ scheduled decode --
-// With a launch list, decode rows run as "head groups".  The (row, slice)
-// pairs of all decode rows are laid end to end and cut into equal ranges,
-// one per group; work-group g = q * Hkv + i streams kv head (i + q) % Hkv of
-// group q's range.  The Hkv work-groups of a group read the same blocks in the
-// same order at about the same time, each its own head's rows, so every K/V
-// block is fetched whole within a short window (on MI355X that reads 7-9%
-// faster than one kv head at a time, measured on the 64-row GQA pattern).
-// Heads rotate with the group so that every XCD (g % 8) streams every head:
-// kv heads at some byte offsets of a token's row read slower, and an XCD
-// holding one such head for the whole launch would end late.
-//
-// A group's range is a list of pieces: whole rows, plus at most one cut row
-// at each end.  At start the work-group copies its piece descriptors and the
-// physical block of every slice of its range into LDS; after that a wave's
-// loop touches global memory only for K/V.  The waves claim slices one at a
-// time from one LDS counter in piece order (all waves share every piece, and
-// the work-group ends when its last slice is computed), with two slices in
-// flight per wave (head_dim <= 128).  A wave keeps one online-softmax state;
-// when its next slice belongs to another piece it folds the state into that
-// piece's LDS accumulator ("bank", a ring of dec_banks of them: piece p uses
-// bank p % dec_banks, which is handed to piece p + banks when p is
-// finished).  The wave that folds a piece's last slice finishes it: a whole
-// row's output is written at once; a cut row leaves a partial (LSE, O) in
-// the workspace, and the last of the row's pieces to finish combines them.
-// The partials are published with device-coherent (sc1) stores, one wait for
-// their completion and one agent-scope atomic per piece; the combining
-// work-group reads them with sc1 loads.  No release fence is needed (on
-// gfx950 that is a whole-L2 write-back), and no wave ever waits for another
-// work-group.  Cut pieces come first in a work-group's list, so this happens
-// while the rest of the range is still streaming.
-//
-// Decode section of a launch list (int4 units, two per unit):
-//   unit 0:            (work-groups, pieces, empty rows, max slices of a
-//                       work-group), (max pieces of a work-group, 0, 0, 0)
-//   1 .. work-groups:  (first piece, pieces, slices, kv head), (group, 0, 0, 0)
-//   pieces, 2 units:   (row, first slice, end slice, row pieces | piece << 16),
-//                      (query token, visible keys, cut row index or -1,
-//                       first row partial of the cut row),
-//                      (first slice of the piece in its work-group's order,
-//                       0, 0, 0), (0, 0, 0, 0)
-//   empty rows:        (query token, 0, 0, 0), (0, 0, 0, 0)
-// A cut row c keeps counters [c * Hkv, (c + 1) * Hkv) (zero between calls:
-// its last piece resets them) and row partials [first, first + pieces), each
-// Hkv partial slots of G (LSE, O).
-constexpr int kDec2MaxBanks = 8;
-constexpr int kDec2Header = 32;            // ints of control words at the start of its LDS
-constexpr int kDec2MaxSlices = 4096;       // slices of one work-group's range
-constexpr int kDec2MaxPieces = 256;        // pieces of one work-group's range
-constexpr int kSpinLimit = 1 << 22;        // bound on every wait (none should come close)
-
-// Floats of one accumulator bank: per-wave slots (O [W][G][D], reference and
-// sum [W][G] each), or one shared accumulator (O [G][D], max and sum [G]);
-// a multiple of 4 so every bank starts 16-byte aligned.
-__host__ __device__ constexpr int64_t decode2_bank_floats(bool slots, int64_t W, int64_t G, int64_t D) {
-  return slots ? W * G * D + (2 * W * G + 3) / 4 * 4 : G * D + (2 * G + 3) / 4 * 4;
-}
-
-// LDS bytes of a scheduled-decode work-group: control words, piece table
-// (3 int4 per piece), Q of every piece, slice table (int2 per slice) and
-// `banks` accumulator banks.
-__host__ __device__ constexpr int64_t decode2_lds_bytes(int64_t banks, bool slots, int64_t W, int64_t G,
-                                                        int64_t D, int64_t max_slices, int64_t max_pieces) {
-  return 4 * kDec2Header + 48 * max_pieces + 2 * max_pieces * G * D + 8 * ((max_slices + 1) / 2 * 2) +
-         4 * banks * decode2_bank_floats(slots, W, G, D);
-}
-
-// Waves of a scheduled-decode work-group: 16 (one work-group per CU, four
-// waves per SIMD, 128 VGPRs each) for head_dim <= 128; 8 for head_dim 256,
-// whose O accumulator and K/V slice need twice the registers.
-constexpr int decode2_waves(int64_t D) { return D <= 128 ? 8 : 8; }
-
-__device__ inline int lds_load_relaxed(const int* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-}
-
-template <class TT, int D>
-__global__ void __launch_bounds__(64 * decode2_waves(D))
-attn_decode2_kernel(const AttnArgs a) {
-  constexpr int W = decode2_waves(D);
-  extern __shared__ float smem[];
-  using st = uint16_t;
-  using WA = WaveAttn<TT, D, 1>;
-  constexpr int EPL = WA::EPL;            // head_dim values per lane per j
-  constexpr int RUN = 4 * EPL;            // contiguous head_dim values a lane holds
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int lane = threadIdx.x & 63;
-  const int n = lane & 15, g = lane >> 4;
-  const int G = a.G;
-  const int NB = a.dec_banks;
-  const bool slots = a.dec_slot_mode != 0;  // per-wave slots, else a locked shared accumulator
-  const bool mrow_ok = n < G;             // this lane's m-row is a query head
-
-  const int4* sec = a.dsched;
-  const int4 top = sec[0], top2 = sec[1];
-  const int nwg = __builtin_amdgcn_readfirstlane(top.x);
-  const int npieces_all = __builtin_amdgcn_readfirstlane(top.y);
-  const int nempty = __builtin_amdgcn_readfirstlane(top.z);
-  const int maxs = __builtin_amdgcn_readfirstlane(top.w);
-  const int maxp = __builtin_amdgcn_readfirstlane(top2.x);
-  const int4 hdr = sec[2 * (1 + static_cast<int64_t>(blockIdx.x))];
-  const int poff = __builtin_amdgcn_readfirstlane(hdr.x);
-  const int pcnt = __builtin_amdgcn_readfirstlane(hdr.y);
-  const int total = __builtin_amdgcn_readfirstlane(hdr.z);
-  const int kvh = __builtin_amdgcn_readfirstlane(hdr.w);  // (work-group + group) % Hkv: every XCD sees every head
-  const int4* pieces = sec + 2 * (1 + static_cast<int64_t>(nwg));
-  const int4* empties = pieces + 4 * static_cast<int64_t>(npieces_all);
-
-  int* ctl = reinterpret_cast<int*>(smem);        // [0] claim counter
-  int* owner = ctl + 2;                           // [kDec2MaxBanks] piece a bank holds
-  int* done = owner + kDec2MaxBanks;              // slices folded into the bank
-  int* lock = done + kDec2MaxBanks;               // shared-accumulator mode only
-  int4* ptab = reinterpret_cast<int4*>(smem + kDec2Header);  // [maxp][3] piece descriptors
-  st* qtab = reinterpret_cast<st*>(ptab + 3 * maxp);         // [maxp][G][D] Q of each piece
-  int2* stab = reinterpret_cast<int2*>(qtab + static_cast<int64_t>(maxp) * G * D);  // [maxs] (block, piece)
-  float* banks = reinterpret_cast<float*>(stab + (maxs + 1) / 2 * 2);
-  const int bank_floats = static_cast<int>(decode2_bank_floats(slots, W, G, D));
-  // Bank b: O (slot w, m-row n, head_dim d) at bo(b)[(w * G + n) * D + d],
-  // reference and sum at bm(b)[w * G + n], bl(b)[w * G + n] (w = 0 when shared).
-  const int nsl_w = slots ? W : 1;
-  auto bo = [&](int b) __attribute__((always_inline)) { return banks + static_cast<int64_t>(b) * bank_floats; };
-  auto bm = [&](int b) __attribute__((always_inline)) { return bo(b) + nsl_w * G * D; };
-  auto bl = [&](int b) __attribute__((always_inline)) { return bm(b) + nsl_w * G; };
-
-  const bool ok_wg = static_cast<int>(blockIdx.x) < nwg && kvh >= 0 && kvh < a.Hkv && pcnt >= 0 &&
-                     pcnt <= maxp && total >= 0 && total <= maxs && poff >= 0 && poff + pcnt <= npieces_all &&
-                     NB >= 1 && NB <= kDec2MaxBanks;
-  const int np_wg = ok_wg ? pcnt : 0;
-  const int total_wg = ok_wg ? total : 0;
-
-  // ---- set-up: piece table; banks empty; Q of every piece; slice table;
-  // rows with no visible key ----
-  for (int i = threadIdx.x; i < 3 * np_wg; i += blockDim.x)
-    ptab[i] = pieces[4 * static_cast<int64_t>(poff + i / 3) + i % 3];
-  for (int i = threadIdx.x; i < NB * bank_floats; i += blockDim.x) banks[i] = 0.f;
-  if (threadIdx.x < kDec2MaxBanks) {
-    owner[threadIdx.x] = static_cast<int>(threadIdx.x) < min(NB, np_wg) ? static_cast<int>(threadIdx.x) : -1;
-    lock[threadIdx.x] = 0;
-    done[threadIdx.x] = 0;
-  }
-  if (threadIdx.x == 0) ctl[0] = 0;
-  for (int e = blockIdx.x; e < nempty; e += max(nwg, 1)) {
-    const int64_t t = empties[2 * static_cast<int64_t>(e)].x;
-    if (t < 0 || t >= a.total_q) continue;
-    for (int i = threadIdx.x; i < a.Hq * (D / 8); i += blockDim.x) {
-      const int h = i / (D / 8), d8 = i % (D / 8);
-      *reinterpret_cast<u32x4*>(static_cast<st*>(a.o) + t * a.o_st + static_cast<int64_t>(h) * a.o_sh + 8 * d8) =
-          u32x4{0u, 0u, 0u, 0u};
-      if (a.lse && d8 == 0) a.lse[t * a.l_st + static_cast<int64_t>(h) * a.l_sh] = -INFINITY;
-    }
-  }
-  __syncthreads();
-  for (int b = 0; b < NB; ++b)  // references start at -inf: an empty slot or bank
-    for (int i = threadIdx.x; i < nsl_w * G; i += blockDim.x) bm(b)[i] = -INFINITY;
-  for (int c = threadIdx.x; c < np_wg * G * (D / 8); c += blockDim.x) {
-    const int p = c / (G * (D / 8)), r = c % (G * (D / 8));
-    const int hh = r / (D / 8), d8 = r % (D / 8);
-    const int64_t qs = ptab[3 * p + 1].x;
-    u32x4 v = {0u, 0u, 0u, 0u};
-    if (qs >= 0 && qs < a.total_q)
-      v = *reinterpret_cast<const u32x4*>(static_cast<const st*>(a.q) + qs * a.q_st +
-                                          static_cast<int64_t>(kvh * G + hh) * a.q_sh + 8 * d8);
-    *reinterpret_cast<u32x4*>(qtab + (static_cast<int64_t>(p) * G + hh) * D + 8 * d8) = v;
-  }
-  const int bs = a.bs;
-  for (int j = threadIdx.x; j < total_wg; j += blockDim.x) {
-    int lo = 0, hi = np_wg - 1;  // last piece whose first slice is <= j
-    while (lo < hi) {
-      const int mid = (lo + hi + 1) >> 1;
-      if (ptab[3 * mid + 2].x <= j) lo = mid;
-      else hi = mid - 1;
-    }
-    const int4 d0 = ptab[3 * lo];
-    const int64_t tok = 16 * static_cast<int64_t>(d0.y + (j - ptab[3 * lo + 2].x));
-    const int64_t lb = tok / bs;
-    int64_t id = (d0.x >= 0 && lb < a.bt_stride) ? a.bt[static_cast<int64_t>(d0.x) * a.bt_stride + lb] : 0;
-    id = id < 0 ? 0 : (id >= a.num_blocks ? a.num_blocks - 1 : id);
-    stab[j] = int2{static_cast<int>(id), lo};
-  }
-  __syncthreads();
-  if (np_wg == 0) return;
-
-  auto claim = [&]() __attribute__((always_inline)) -> int {
-    int r = 0;
-    if (lane == 0) r = atomicAdd(&ctl[0], 1);
-    return __builtin_amdgcn_readfirstlane(r);
-  };
-  auto rfl4 = [](int4 v) __attribute__((always_inline)) {
-    return int4{__builtin_amdgcn_readfirstlane(v.x), __builtin_amdgcn_readfirstlane(v.y),
-                __builtin_amdgcn_readfirstlane(v.z), __builtin_amdgcn_readfirstlane(v.w)};
-  };
-
-  // ---- the state this wave holds: piece sp (-1: none), its descriptor ----
-  int sp = -1, s_nsl = 0;
-  int4 s0d = int4{0, 0, 0, 0}, s1d = int4{0, 0, 0, 0};
-  WA wa;
-  wa.n = n;  // lane coordinates: the first loads are issued before any state starts
-  wa.g = g;
-
-  // Output of a finished piece, normalised: this lane's RUN values and the
-  // m-row's log2-domain LSE.  A whole row's final O and LSE are written at
-  // once.  A cut row's partial is published without stalling the wave: its
-  // sc1 stores are issued now; a few slices later, once loads issued after
-  // them have returned (so the stores have completed), the agent-scope atomic
-  // counts this piece in; a few slices after that its result says whether
-  // this piece was the row's last, and then the wave combines the partials.
-  // One publication is in flight per wave (a second one first finishes it).
-  int pub_state = 0, pub_wait = 0, pub_old = 0;  // 1: stores issued, 2: atomic issued
-  int pub_np = 0, pub_crow = 0, pub_prow = 0;
-  int64_t pub_t = 0;
-  const __amdgpu_buffer_rsrc_t ro = block_rsrc(a.ws_o, static_cast<int>(a.num_partials * G * D * 4));
-  const __amdgpu_buffer_rsrc_t rl = block_rsrc(a.ws_lse, static_cast<int>(a.num_partials * G * 4));
-  // Combines every piece's partial of cut row pub_crow (sc1 loads see the
-  // other work-groups' published stores).  All 64 lanes take part: lane l
-  // owns floats [l * F, (l + 1) * F) of a partial's [G][D] block, in chunks
-  // of at most 16 (one head per chunk: D is a multiple of 16 and of F).
-  auto combine = [&]() __attribute__((always_inline)) {
-    const int F = G * D / 64;
-    const int CF = F < 16 ? F : 16;
-    const int np = pub_np, prow = pub_prow;
-    const int64_t t = pub_t;
-    for (int f0 = lane * F; f0 < (lane + 1) * F; f0 += CF) {
-      const int hh = f0 / D, d0c = f0 % D;
-      float m = -INFINITY, l = 0.f;
-      float acc[16];
-#pragma unroll
-      for (int i = 0; i < 16; ++i) acc[i] = 0.f;
-      for (int p = 0; p < np; ++p) {
-        const int64_t sl2 = (static_cast<int64_t>(prow) + p) * a.Hkv + kvh;
-        if (sl2 >= a.num_partials) continue;
-        const float lp = __uint_as_float(
-            __builtin_amdgcn_raw_buffer_load_b32(rl, static_cast<int>((sl2 * G + hh) * 4), 0, kSc1));
-        float v[16];
-        const int off = static_cast<int>((sl2 * G * D + f0) * 4);
-        if (CF >= 4) {
-#pragma unroll
-          for (int c = 0; c < 4; ++c) {
-            const f32x4 x = c * 4 < CF ? __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(ro, off + 16 * c, 0, kSc1))
-                                       : f32x4{0.f, 0.f, 0.f, 0.f};
-            v[4 * c] = x.x; v[4 * c + 1] = x.y; v[4 * c + 2] = x.z; v[4 * c + 3] = x.w;
-          }
-        } else {
-#pragma unroll
-          for (int i = 0; i < 16; ++i)
-            v[i] = i < CF ? __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(ro, off + 4 * i, 0, kSc1)) : 0.f;
-        }
-        if (lp == -INFINITY) continue;
-        const float mn = fmaxf(m, lp);
-        const float ca = fast_exp2(m - mn), cw = fast_exp2(lp - mn);  // ca = 0 while m is -inf
-        l = l * ca + cw;
-#pragma unroll
-        for (int i = 0; i < 16; ++i) acc[i] = acc[i] * ca + v[i] * cw;
-        m = mn;
-      }
-      const float inv = l > 0.f ? 1.f / l : 0.f;
-      if (t < 0 || t >= a.total_q) continue;
-      const int hq = kvh * G + hh;
-      st* op = static_cast<st*>(a.o) + t * a.o_st + static_cast<int64_t>(hq) * a.o_sh + d0c;
-      if (CF >= 8) {
-#pragma unroll
-        for (int c = 0; c < 2; ++c)
-          if (c * 8 < CF)
-            *reinterpret_cast<u32x4*>(op + 8 * c) =
-                u32x4{TT::pack2(acc[8 * c] * inv, acc[8 * c + 1] * inv), TT::pack2(acc[8 * c + 2] * inv, acc[8 * c + 3] * inv),
-                      TT::pack2(acc[8 * c + 4] * inv, acc[8 * c + 5] * inv), TT::pack2(acc[8 * c + 6] * inv, acc[8 * c + 7] * inv)};
-      } else {
-        for (int i = 0; i < CF; ++i) op[i] = TT::from_float(acc[i] * inv);
-      }
-      if (a.lse && d0c == 0)
-        a.lse[t * a.l_st + static_cast<int64_t>(hq) * a.l_sh] = l > 0.f ? (m + __log2f(l)) * kLn2 : -INFINITY;
-    }
-    if (lane == 0)
-      __hip_atomic_store(a.merge_ctr + static_cast<int64_t>(pub_crow) * a.Hkv + kvh, 0, __ATOMIC_RELAXED,
-                         __HIP_MEMORY_SCOPE_AGENT);
-  };
-  // Moves the publication on: `sync` finishes it now (waiting for its
-  // memory operations), otherwise a stage starts only when enough slices
-  // have passed for it not to wait.
-  auto publish_step = [&](bool sync) __attribute__((always_inline)) {
-    if (pub_state == 1 && (sync || ++pub_wait >= 3)) {
-      // Every load issued after the stores has returned but the newest
-      // slice's, so the stores have completed (memory operations of a wave
-      // complete in order).
-      if (sync) __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
-      else __asm__ volatile("s_waitcnt vmcnt(8)" ::: "memory");
-      int old = 0;
-      if (lane == 0)
-        old = __hip_atomic_fetch_add(a.merge_ctr + static_cast<int64_t>(pub_crow) * a.Hkv + kvh, 1, __ATOMIC_RELAXED,
-                                     __HIP_MEMORY_SCOPE_AGENT);
-      pub_old = old;
-      pub_state = 2;
-      pub_wait = 0;
-      if (!sync) return;
-    }
-    if (pub_state == 2 && (sync || ++pub_wait >= 3)) {
-      pub_state = 0;
-      if (__builtin_amdgcn_readfirstlane(pub_old) == pub_np - 1) combine();
-    }
-  };
-  auto emit = [&](const int4& d0, const int4& d1, const float (&ov)[RUN], float lse2) __attribute__((always_inline)) {
-    const int np = d0.w & 0xffff, pidx = (d0.w >> 16) & 0xffff;
-    const int64_t t = d1.x;
-    const int h = kvh * G + n;
-    if (np <= 1) {
-      if (!mrow_ok || t < 0 || t >= a.total_q) return;
-      st* op = static_cast<st*>(a.o) + t * a.o_st + static_cast<int64_t>(h) * a.o_sh + RUN * g;
-#pragma unroll
-      for (int c = 0; c < RUN / 8; ++c)
-        *reinterpret_cast<u32x4*>(op + 8 * c) =
-            u32x4{TT::pack2(ov[8 * c], ov[8 * c + 1]), TT::pack2(ov[8 * c + 2], ov[8 * c + 3]),
-                  TT::pack2(ov[8 * c + 4], ov[8 * c + 5]), TT::pack2(ov[8 * c + 6], ov[8 * c + 7])};
-      if (a.lse && g == 0)
-        a.lse[t * a.l_st + static_cast<int64_t>(h) * a.l_sh] = lse2 == -INFINITY ? -INFINITY : lse2 * kLn2;
-      return;
-    }
-    const int crow = d1.z, prow = d1.w;
-    const int64_t slot = (static_cast<int64_t>(prow) + pidx) * a.Hkv + kvh;
-    if (crow < 0 || prow < 0 || slot >= a.num_partials) return;
-    if (pub_state != 0) publish_step(true);
-    if (mrow_ok) {
-      const int off = static_cast<int>(((slot * G + n) * D + RUN * g) * 4);
-#pragma unroll
-      for (int c = 0; c < RUN / 4; ++c)
-        __builtin_amdgcn_raw_buffer_store_b128(
-            __builtin_bit_cast(u32x4, f32x4{ov[4 * c], ov[4 * c + 1], ov[4 * c + 2], ov[4 * c + 3]}), ro,
-            off + 16 * c, 0, kSc1);
-      if (g == 0)
-        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(lse2), rl, static_cast<int>((slot * G + n) * 4), 0, kSc1);
-    }
-    pub_state = 1;
-    pub_wait = 0;
-    pub_np = np;
-    pub_crow = crow;
-    pub_prow = prow;
-    pub_t = t;
-  };
-
-  // Folds the wave's state for piece sp (s_nsl slices) into its bank: its own
-  // slot (no lock), or the shared accumulator under the bank's lock.  The
-  // wave that completes the piece combines the bank, empties it, hands it on
-  // and emits the piece.
-  auto fold = [&]() __attribute__((always_inline)) {
-    float lt[1];
-    wa.row_sums(lt);
-    const int b = sp % NB;
-    const int w = slots ? wave : 0;
-    if (!slots) {
-      for (int it = 0;; ++it) {  // lock the bank
-        int got = 0;
-        if (lane == 0) got = atomicCAS(&lock[b], 0, 1) == 0 ? 1 : 0;
-        if (__builtin_amdgcn_readfirstlane(got) || it > kSpinLimit) break;
-        __builtin_amdgcn_s_sleep(1);
-      }
-      __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    }
-    if (mrow_ok) {
-      const int ai = w * G + n;
-      float* po = bo(b) + static_cast<int64_t>(ai) * D + RUN * g;
-      const float wm = wa.m[0];
-      if (slots) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-#pragma unroll
-          for (int e = 0; e < EPL; e += 4)
-            *reinterpret_cast<f32x4*>(po + EPL * j + e) =
-                f32x4{wa.o[0][e][j], wa.o[0][e + 1][j], wa.o[0][e + 2][j], wa.o[0][e + 3][j]};
-        if (g == 0) {
-          bm(b)[ai] = wm;
-          bl(b)[ai] = lt[0];
-        }
-      } else {
-        const float am = bm(b)[ai], al = bl(b)[ai];
-        const float mn = fmaxf(am, wm);
-        const float ca = am == -INFINITY ? 0.f : fast_exp2(am - mn);
-        const float cw = wm == -INFINITY ? 0.f : fast_exp2(wm - mn);
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-#pragma unroll
-          for (int e = 0; e < EPL; e += 4) {
-            f32x4 v = *reinterpret_cast<const f32x4*>(po + EPL * j + e);
-            v = v * ca + f32x4{wa.o[0][e][j], wa.o[0][e + 1][j], wa.o[0][e + 2][j], wa.o[0][e + 3][j]} * cw;
-            *reinterpret_cast<f32x4*>(po + EPL * j + e) = v;
-          }
-        if (g == 0) {
-          bm(b)[ai] = mn;
-          bl(b)[ai] = al * ca + lt[0] * cw;
-        }
-      }
-    }
-    __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    int old = 0;
-    if (lane == 0) {
-      if (!slots) __hip_atomic_store(&lock[b], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-      old = atomicAdd(&done[b], s_nsl);
-    }
-    old = __builtin_amdgcn_readfirstlane(old);
-    if (old + s_nsl != s0d.z - s0d.y) return;
-    // ---- the piece is complete: combine, empty the bank, hand it on ----
-    __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    float ov[RUN];
-    float lse2 = -INFINITY;
-#pragma unroll
-    for (int i = 0; i < RUN; ++i) ov[i] = 0.f;
-    if (mrow_ok) {
-      float mx = -INFINITY;
-      for (int w2 = 0; w2 < nsl_w; ++w2) mx = fmaxf(mx, bm(b)[w2 * G + n]);
-      float lsum = 0.f;
-      if (mx != -INFINITY) {
-        for (int w2 = 0; w2 < nsl_w; ++w2) {
-          const int ai = w2 * G + n;
-          const float mw = bm(b)[ai];
-          if (mw == -INFINITY) continue;  // a slot no wave wrote for this piece
-          const float c = fast_exp2(mw - mx);
-          lsum += c * bl(b)[ai];
-          const float* po = bo(b) + static_cast<int64_t>(ai) * D + RUN * g;
-#pragma unroll
-          for (int k = 0; k < RUN / 4; ++k) {
-            const f32x4 v = *reinterpret_cast<const f32x4*>(po + 4 * k);
-            ov[4 * k] += c * v.x; ov[4 * k + 1] += c * v.y; ov[4 * k + 2] += c * v.z; ov[4 * k + 3] += c * v.w;
-          }
-        }
-      }
-      const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
-#pragma unroll
-      for (int i = 0; i < RUN; ++i) ov[i] *= inv;
-      lse2 = lsum > 0.f ? mx + __log2f(lsum) : -INFINITY;
-      if (!slots) {  // the shared accumulator restarts at zero
-        float* po = bo(b) + static_cast<int64_t>(n) * D + RUN * g;
-#pragma unroll
-        for (int k = 0; k < RUN / 4; ++k) *reinterpret_cast<f32x4*>(po + 4 * k) = f32x4{0.f, 0.f, 0.f, 0.f};
-        if (g == 0) bl(b)[n] = 0.f;
-      }
-      if (g == 0)
-        for (int w2 = 0; w2 < nsl_w; ++w2) bm(b)[w2 * G + n] = -INFINITY;
-    }
-    __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    if (lane == 0) {
-      done[b] = 0;
-      __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-      const int nxt = sp + NB;
-      __hip_atomic_store(&owner[b], nxt < np_wg ? nxt : -1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-    }
-    emit(s0d, s1d, ov, lse2);
-  };
-
-  // Starts a state for piece p: waits until its bank is handed to it, then
-  // takes its Q.
-  auto start = [&](int p) __attribute__((always_inline)) {
-    const int b = p % NB;
-    for (int it = 0; __builtin_amdgcn_readfirstlane(lds_load_relaxed(&owner[b])) != p && it <= kSpinLimit; ++it)
-      __builtin_amdgcn_s_sleep(2);
-    __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    wa.mq[0] = 0;
-    wa.mh[0] = kvh * G + (n % G);
-    wa.mval[0] = mrow_ok;
-    wa.qpos[0] = mrow_ok ? INT_MAX : -1;
-    const st* qb = qtab + (static_cast<int64_t>(p) * G + (mrow_ok ? n : 0)) * D;
-#pragma unroll
-    for (int c = 0; c < WA::NC; ++c)
-      wa.qf[0][c] = mrow_ok ? *reinterpret_cast<const u32x4*>(qb + 8 * (4 * c + g)) : u32x4{0u, 0u, 0u, 0u};
-    wa.m[0] = -FLT_MAX;
-    wa.l[0] = 0.f;
-#pragma unroll
-    for (int e = 0; e < EPL; ++e) wa.o[0][e] = f32x4{0.f, 0.f, 0.f, 0.f};
-    sp = __builtin_amdgcn_readfirstlane(p);
-    s_nsl = 0;
-    s0d = rfl4(ptab[3 * p]);
-    s1d = rfl4(ptab[3 * p + 1]);
-  };
-
-  // ---- main loop.  A slice's loads are issued into one buffer while the
-  // other buffer's slice is computed; past the last slice the loads go
-  // through an empty descriptor (no memory access), so every step issues the
-  // same loads and the wait for the older buffer never drains the newer one.
-  struct Pending {
-    int ts, kend, piece;
-    bool valid;
-  };
-  auto issue = [&](KVSlice<D>& T, Pending& pd) __attribute__((always_inline)) {
-    const int j = claim();
-    pd.valid = j < total_wg;
-    const int2 e = stab[pd.valid ? j : 0];
-    const int p = __builtin_amdgcn_readfirstlane(e.y);
-    const int64_t id = __builtin_amdgcn_readfirstlane(e.x);
-    const int4 d0 = rfl4(ptab[3 * p]);
-    const int first = __builtin_amdgcn_readfirstlane(ptab[3 * p + 2].x);
-    const int sl = d0.y + (j - first);
-    const int tok = 16 * sl;
-    const int bo_tok = bs == 16 ? 0 : tok % bs;
-    pd.ts = tok;
-    pd.kend = __builtin_amdgcn_readfirstlane(ptab[3 * p + 1].y);
-    pd.piece = p;
-    const st* kb = static_cast<const st*>(a.k) + static_cast<int64_t>(kvh) * a.k_sh + id * a.k_sb;
-    const st* vb = static_cast<const st*>(a.v) + static_cast<int64_t>(kvh) * a.v_sh + id * a.v_sb;
-    wa.load_slice_bounded(a, kb, vb, bo_tok, pd.valid ? 1 : 0, T);
-  };
-  // The slice is computed on two separate paths: joining the piece-switch
-  // path (whose loads and waits differ) before the compute makes the
-  // compiler wait for both buffers instead of one.
-  auto consume = [&](KVSlice<D>& T, const Pending& pd) __attribute__((always_inline)) {
-    if (__builtin_amdgcn_readfirstlane(pd.piece) != sp) {
-      if (sp >= 0) fold();
-      start(pd.piece);
-      wa.compute_slice_lazy(a, pd.ts, pd.kend, T);
-    } else {
-      wa.compute_slice_lazy(a, pd.ts, pd.kend, T);
-    }
-    ++s_nsl;
-    if (pub_state != 0) publish_step(false);
-  };
-  if constexpr (D <= 128) {
-    KVSlice<D> T0, T1;
-    Pending p0{0, 0, 0, false}, p1{0, 0, 0, false};
-    issue(T0, p0);
-    issue(T1, p1);
-    while (p0.valid) {
-      consume(T0, p0);
-      issue(T0, p0);
-      if (!p1.valid) break;
-      consume(T1, p1);
-      issue(T1, p1);
-    }
-  } else {  // head_dim 256: one slice buffer (two would not fit the registers)
-    KVSlice<D> T0;
-    Pending p0{0, 0, 0, false};
-    issue(T0, p0);
-    while (p0.valid) {
-      consume(T0, p0);
-      issue(T0, p0);
-    }
-  }
-  if (sp >= 0) fold();
-  if (pub_state != 0) publish_step(true);
-}
-
-// Combines the partitions of grid-mode decode rows: the grid is (head_dim
+// Combines the parts of split decode segments: (row, kv head) pieces that
+// ran in different work-groups and left (LSE, O) partials.  With a schedule,
+// work-group u takes merge unit u = (query token, kv head, parts, first
+// partial index), each lane 8 head_dim values of one of the G query heads;
+// the kMergeWaves waves of the work-group fold a share of the parts each and
+// combine their states through LDS.  Without one, the grid is (head_dim
 // chunks, rows) of one-wave work-groups, and a row's parts are the fixed
-// partitions of part_tokens keys, recomputed as the decode kernel did.  Each
-// lane folds 8 head_dim values of one query head over the row's partitions,
-// kBatch of them at a time.  (kMergeWaves > 1 splits the partitions over the
-// waves of a work-group and combines their states through LDS.)
+// partitions of part_tokens keys, recomputed as the decode kernel did.
 constexpr int kMergeWaves = 4;
 
 template <class TT, int D>
@@ -1461,7 +867,15 @@ attn_merge_kernel(const AttnArgs a) {
   const int wv = static_cast<int>(threadIdx.x >> 6), nwv = static_cast<int>(blockDim.x >> 6);
   int64_t t, base;
   int kvh, nparts, it0, step;
-  {
+  if (a.merge_units) {
+    const int4 u = a.merge_units[2 * static_cast<int64_t>(blockIdx.x)];
+    t = u.x;
+    kvh = u.y;
+    nparts = u.z;
+    base = u.w;
+    it0 = threadIdx.x & 63;
+    step = 64;
+  } else {
     const int row = blockIdx.y;
     if (a.q_lens[row] != 1) return;
     const int idx = blockIdx.x * 64 + threadIdx.x;
@@ -1947,26 +1361,32 @@ attn_generic_kernel(const AttnArgs a) {
 
 // ------------------------------------------------------------------ host --
 
-// LDS of one work-group: 64 KiB by default, up to the 160 KiB of a gfx950 CU
-// for kernels that raise their limit (hipFuncSetAttribute).
-constexpr int64_t kDefaultLdsBytes = 64 * 1024;
+// LDS of a decode work-group: 64 KiB, or up to the 160 KiB of a gfx950 CU when
+// one slot per wave needs more (query groups of 16 heads at head_dim 128, 8 or
+// more at 256; 8 waves then fit at every head_dim and group size).
+constexpr int64_t kMaxLdsBytes = 64 * 1024;
+constexpr int64_t kCuLdsBytes = 160 * 1024;
 #ifndef KVHOT_MAX_DECODE_WAVES
 #define KVHOT_MAX_DECODE_WAVES 16
 #endif
 
-// Waves per grid-mode decode work-group: 16 (head_dim <= 128, whose registers
-// allow 4 waves per SIMD) when one slot per wave fits in 64 KiB of LDS, else 8.
+// Waves per decode work-group: 16 (head_dim <= 128, whose registers allow 4
+// waves per SIMD) when one slot per wave fits in 64 KiB of LDS, else 8.
 static int decode_waves(int64_t G, int64_t D) {
-  if (KVHOT_MAX_DECODE_WAVES >= 16 && D <= 128 && decode_lds_words(16, 16, G, D) * 4 <= kDefaultLdsBytes)
+  if (KVHOT_MAX_DECODE_WAVES >= 16 && D <= 128 && decode_lds_words(16, 16, G, D) * 4 <= kMaxLdsBytes)
     return 16;
   return 8;
 }
 
-// LDS slots of a grid-mode decode work-group of W waves: one per wave plus a
-// pool of up to W more for waves that move on to other segments, as 64 KiB of
-// LDS allows (a work-group whose W slots alone need more takes exactly those).
+// LDS bytes a decode work-group of W waves may use (see kMaxLdsBytes).
+static int64_t decode_lds_limit(int W, int64_t G, int64_t D) {
+  return decode_lds_words(W, W, G, D) * 4 <= kMaxLdsBytes ? kMaxLdsBytes : kCuLdsBytes;
+}
+
+// LDS slots of a decode work-group of W waves: one per wave plus a pool of up
+// to W more for waves that move on to other segments, as LDS allows.
 static int decode_slots(int W, int64_t G, int64_t D) {
-  const int64_t spare = kDefaultLdsBytes / 4 - decode_lds_words(W, W, G, D);
+  const int64_t spare = decode_lds_limit(W, G, D) / 4 - decode_lds_words(W, W, G, D);
   const int64_t per_slot = G * D + G + 4;
   return W + static_cast<int>(std::max<int64_t>(0, std::min<int64_t>(W, spare / per_slot)));
 }
@@ -1974,250 +1394,14 @@ static int decode_slots(int W, int64_t G, int64_t D) {
 // Bytes of one split-K partial: the normalised O and LSE of G query heads.
 static int64_t partial_bytes(int64_t G, int64_t D) { return G * (D + 1) * 4; }
 
-// ------------------------------------------------ scheduled decode (host) --
-
-// Bytes at the start of every workspace that hold the scheduled decode's
-// cut-row counters (zero between calls), then the split-K partials.
-constexpr int64_t kCounterBytes = KVHOT_WORKSPACE_COUNTER_BYTES;
-constexpr int64_t kMaxCounters = kCounterBytes / 4;
-// Shortest piece a row is cut into (slices): a shorter tail is kept whole.
-constexpr int64_t kMinPieceSlices = 4;
-// Fewest slices per wave a group's range is cut for: below it a work-group's
-// waves would idle.
-constexpr int64_t kMinGroupSlicesPerWave = 2;
-
-// Accumulator banks of a scheduled-decode work-group with these tables:
-// per-wave slots when 4 or 8 banks of them fit the 160 KiB of a gfx950 CU's
-// LDS (a scheduled-decode work-group has the CU to itself: its registers
-// allow one), else a shared accumulator per bank; 8 banks when they fit, else
-// 4.  Returns banks | slots << 8, or 0 when nothing fits.
-static int decode2_banks(int64_t G, int64_t D, int64_t max_slices, int64_t max_pieces) {
-  constexpr int64_t kLimit = 160 * 1024;
-  const int64_t W = decode2_waves(D);
-  for (bool slots : {true, false})
-    for (int banks : {8, 4})
-      if (decode2_lds_bytes(banks, slots, W, G, D, max_slices, max_pieces) <= kLimit) return banks | (slots ? 256 : 0);
-  return 0;
-}
-
-// Scheduled-decode work-groups the device holds at once (256, one per CU of
-// an MI355X, when no device can be queried).
-template <class TT, int D>
-static int64_t resident_decode2_groups() {
-  int dev = 0, cus = 0, per = 0;
-  const size_t lds = 96 * 1024;
-  if (hipGetDevice(&dev) != hipSuccess ||
-      hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_decode2_kernel<TT, D>),
-                          hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)) != hipSuccess ||
-      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, attn_decode2_kernel<TT, D>, 64 * decode2_waves(D), lds) !=
-          hipSuccess ||
-      cus <= 0 || per <= 0) {
-    (void)hipGetLastError();
-    return 256;
-  }
-  return static_cast<int64_t>(cus) * per;
-}
-
-template <class TT>
-static int64_t resident_decode2_groups(int64_t D) {
-  if (D == 64) return resident_decode2_groups<TT, 64>();
-  if (D == 128) return resident_decode2_groups<TT, 128>();
-  return resident_decode2_groups<TT, 256>();
-}
-
-struct DecodePlan {
-  std::vector<int4> units;   // the decode section, two int4 per unit
-  int64_t groups = 0;        // work-groups of the decode launch
-  int64_t cut_rows = 0;      // rows cut across work-groups
-  int64_t row_partials = 0;  // partials of the cut rows (each Hkv slots)
-  int64_t lds_bytes = 0;     // dynamic LDS of a decode work-group
-  int banks = 0;             // its accumulator banks | per-wave slots << 8
-};
-
-// Head-group launch list of the decode rows (see attn_decode2_kernel): their
-// (row, slice) pairs, rows in order, are cut into `ngrp` equal ranges (a cut
-// leaves at least kMinPieceSlices on either side, and with given_pt > 0 falls
-// on a multiple of given_pt keys into the row); each range's pieces are listed
-// cut rows first.  A range holds at most kDec2MaxSlices slices and
-// kDec2MaxPieces pieces (more groups are made when needed).  Returns false
-// when a count exceeds its field or the counter area.
-static bool plan_decode2(const int32_t* q_lens, const int32_t* k_lens, const int32_t* q_offs,
-                         const int32_t* q_starts, int64_t rows, int64_t Hkv, int64_t G, int64_t D, bool causal,
-                         int64_t resident_groups, int64_t given_pt, DecodePlan& out) {
-  out = DecodePlan{};
-  std::vector<int64_t> nsl(rows, 0), kend(rows, 0);
-  std::vector<int> empties;
-  int64_t total = 0, live_rows = 0;
-  for (int64_t r = 0; r < rows; ++r) {
-    if (q_lens[r] != 1) continue;
-    const int64_t klen = k_lens[r], off = q_offs[r];
-    kend[r] = std::max<int64_t>(causal ? std::min(klen, off + 1) : klen, 0);
-    nsl[r] = (kend[r] + 15) / 16;
-    if (nsl[r] == 0) empties.push_back(static_cast<int>(r));
-    else ++live_rows;
-    total += nsl[r];
-  }
-  if (total == 0 && empties.empty()) return true;
-  const int64_t pt_sl = given_pt > 0 ? given_pt / 16 : 0;
-  struct Pc {
-    int64_t row, s0, s1;
-  };
-  std::vector<std::vector<Pc>> grp;
-  int64_t ngrp = 0;
-  if (total > 0) {
-    ngrp = std::min(std::max<int64_t>(1, resident_groups / Hkv),
-                    std::max<int64_t>(1, total / (kMinGroupSlicesPerWave * decode2_waves(D))));
-    ngrp = std::max({ngrp, (total + kDec2MaxSlices / 2 - 1) / (kDec2MaxSlices / 2),
-                     (live_rows + kDec2MaxPieces / 2 - 1) / (kDec2MaxPieces / 2)});
-  }
-  for (int attempt = 0; total > 0; ++attempt) {
-    if (attempt > 8 || ngrp > total) return false;
-    const int64_t target = (total + ngrp - 1) / ngrp;
-    grp.assign(static_cast<size_t>(ngrp), {});
-    int64_t q = 0, load = 0;
-    for (int64_t r = 0; r < rows; ++r) {
-      int64_t s = 0, rem = nsl[r];
-      while (rem > 0) {
-        const bool last = q == ngrp - 1;
-        const int64_t space = target - load;
-        if (last || rem <= space) {
-          grp[q].push_back(Pc{r, s, s + rem});
-          load += rem;
-          break;
-        }
-        int64_t take = space;
-        if (pt_sl > 0) take = ((s + take) / pt_sl) * pt_sl - s;
-        if (take < kMinPieceSlices) {  // too little room: the row starts the next range
-          ++q;
-          load = 0;
-          continue;
-        }
-        if (rem - take < kMinPieceSlices) {  // a short tail stays with its row
-          grp[q].push_back(Pc{r, s, s + rem});
-          load += rem;
-          break;
-        }
-        grp[q].push_back(Pc{r, s, s + take});
-        s += take;
-        rem -= take;
-        ++q;
-        load = 0;
-      }
-    }
-    bool fits = true;
-    int64_t ms = 0, mp = 0;
-    for (const auto& gp : grp) {
-      int64_t sl = 0;
-      for (const Pc& pc : gp) sl += pc.s1 - pc.s0;
-      ms = std::max(ms, sl);
-      mp = std::max(mp, static_cast<int64_t>(gp.size()));
-    }
-    fits = ms <= kDec2MaxSlices && mp <= kDec2MaxPieces && decode2_banks(G, D, ms, mp) != 0;
-    if (fits) break;
-    ngrp *= 2;
-  }
-  // Cut rows: their pieces in row order, counters and row partials.
-  std::vector<int64_t> npieces(rows, 0), cut_id(rows, -1), prow(rows, -1);
-  for (const auto& gp : grp)
-    for (const Pc& pc : gp) ++npieces[pc.row];
-  for (int64_t r = 0; r < rows; ++r)
-    if (npieces[r] > 1) {
-      if (npieces[r] > 32767) return false;
-      cut_id[r] = out.cut_rows++;
-      prow[r] = out.row_partials;
-      out.row_partials += npieces[r];
-    }
-  if (out.cut_rows * Hkv > kMaxCounters) return false;
-  if (out.row_partials * Hkv * G * D * 4 >= (int64_t{1} << 31)) return false;
-
-  const int64_t nwg = ngrp > 0 ? ngrp * Hkv : 1;
-  int64_t npc = 0, maxs = 0, maxp = 0;
-  for (const auto& gp : grp) {
-    int64_t sl = 0;
-    for (const Pc& pc : gp) sl += pc.s1 - pc.s0;
-    npc += static_cast<int64_t>(gp.size());
-    maxs = std::max(maxs, sl);
-    maxp = std::max(maxp, static_cast<int64_t>(gp.size()));
-  }
-  if (nwg > 0x7fffffff || 1 + nwg + 2 * npc + static_cast<int64_t>(empties.size()) > (int64_t{1} << 30)) return false;
-  out.banks = decode2_banks(G, D, maxs, maxp);
-  if (out.banks == 0) return false;
-  out.lds_bytes = decode2_lds_bytes(out.banks & 255, (out.banks & 256) != 0, decode2_waves(D), G, D, maxs, maxp);
-  out.groups = nwg;
-  std::vector<int4>& u = out.units;
-  u.reserve(2 * (1 + nwg + 2 * npc + empties.size()));
-  u.push_back(int4{static_cast<int>(nwg), static_cast<int>(npc), static_cast<int>(empties.size()),
-                   static_cast<int>(maxs)});
-  u.push_back(int4{static_cast<int>(maxp), 0, 0, 0});
-  // Headers: work-group q * Hkv + i reads group q's pieces for kv head (i + q) % Hkv.
-  std::vector<int64_t> goff(static_cast<size_t>(ngrp), 0), gsl(static_cast<size_t>(ngrp), 0);
-  int64_t off = 0;
-  for (int64_t g2 = 0; g2 < ngrp; ++g2) {
-    goff[g2] = off;
-    off += static_cast<int64_t>(grp[g2].size());
-    for (const Pc& pc : grp[g2]) gsl[g2] += pc.s1 - pc.s0;
-  }
-  for (int64_t wg = 0; wg < nwg; ++wg) {
-    if (ngrp == 0) {
-      u.push_back(int4{0, 0, 0, 0});
-    } else {
-      const int64_t g2 = wg / Hkv;
-      u.push_back(int4{static_cast<int>(goff[g2]), static_cast<int>(grp[g2].size()), static_cast<int>(gsl[g2]),
-                       static_cast<int>((wg % Hkv + g2) % Hkv)});
-    }
-    u.push_back(int4{static_cast<int>(ngrp > 0 ? wg / Hkv : 0), 0, 0, 0});
-  }
-  // Pieces, cut rows first within each range.  A row's piece index follows
-  // its order along the row.
-  for (auto& gp : grp)
-    std::stable_partition(gp.begin(), gp.end(), [&](const Pc& pc) { return npieces[pc.row] > 1; });
-  std::vector<std::vector<int64_t>> row_piece_s0(rows);
-  for (const auto& gp : grp)
-    for (const Pc& pc : gp) row_piece_s0[pc.row].push_back(pc.s0);
-  for (auto& v : row_piece_s0) std::sort(v.begin(), v.end());
-  for (const auto& gp : grp) {
-    int64_t first = 0;
-    for (const Pc& pc : gp) {
-      const auto& v = row_piece_s0[pc.row];
-      const int64_t idx = std::lower_bound(v.begin(), v.end(), pc.s0) - v.begin();
-      const int64_t np = npieces[pc.row];
-      u.push_back(int4{static_cast<int>(pc.row), static_cast<int>(pc.s0), static_cast<int>(pc.s1),
-                       static_cast<int>(np | (idx << 16))});
-      u.push_back(int4{q_starts[pc.row], static_cast<int>(kend[pc.row]), static_cast<int>(cut_id[pc.row]),
-                       static_cast<int>(np > 1 ? prow[pc.row] : 0)});
-      u.push_back(int4{static_cast<int>(first), 0, 0, 0});
-      u.push_back(int4{0, 0, 0, 0});
-      first += pc.s1 - pc.s0;
-    }
-  }
-  for (int r : empties) {
-    u.push_back(int4{q_starts[r], 0, 0, 0});
-    u.push_back(int4{0, 0, 0, 0});
-  }
-  return true;
-}
-
-template <class TT, int D>
-static void launch_decode2(const AttnArgs& a, int64_t groups, int64_t lds_bytes, hipStream_t stream) {
-  const size_t lds = static_cast<size_t>(lds_bytes);
-  if (lds > 64 * 1024)
-    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_decode2_kernel<TT, D>),
-                              hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
-  hipLaunchKernelGGL((attn_decode2_kernel<TT, D>), dim3(static_cast<uint32_t>(groups)), dim3(64 * decode2_waves(D)), lds,
-                     stream, a);
-}
-
 struct Plan {
   bool mfma = false;     // the MFMA kernels take this shape
   bool grid_ok = false;  // ... also without a schedule (partition count fits the grid)
-  int waves = 0;         // waves per grid-mode decode work-group
+  int waves = 0;         // waves per decode work-group
   int part_tokens = 0;   // keys per decode partition (no schedule)
   int max_parts = 1;
   int64_t partials = 0;  // split-K partials without a schedule
-  int64_t workspace_bytes(int64_t G, int64_t D) const {
-    return partials > 0 ? kCounterBytes + partials * partial_bytes(G, D) : 0;
-  }
+  int64_t workspace_bytes(int64_t G, int64_t D) const { return partials * partial_bytes(G, D); }
 };
 
 static bool mfma_shape_ok(int64_t Hq, int64_t Hkv, int64_t D, int64_t bs, int dtype) {
@@ -2252,6 +1436,278 @@ static Plan make_plan(int64_t rows, int64_t max_q, int64_t max_k, int64_t Hq,
 // and Q 32 at every head_dim, so two waves fit on a SIMD.
 constexpr int prefill_nm(int64_t D) { return D == 64 ? 4 : (D == 128 ? 2 : 1); }
 
+// Decode work-groups the current device holds at once, times their waves
+// (4096 when no device can be queried).
+template <class TT, int D, int W>
+static int decode_groups_per_cu(int64_t G) {
+  int n = 0;
+  const size_t lds = static_cast<size_t>(decode_lds_words(W, decode_slots(W, G, D), G, D) * 4);
+  if ((lds > kMaxLdsBytes &&
+       hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_decode_kernel<TT, D, W>),
+                           hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)) != hipSuccess) ||
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, attn_decode_kernel<TT, D, W>, 64 * W, lds) !=
+          hipSuccess)
+    n = 0;
+  return n;
+}
+
+template <class TT>
+static int decode_groups_per_cu(int64_t D, int W, int64_t G) {
+  if (W == 16) {
+    if (D == 64) return decode_groups_per_cu<TT, 64, 16>(G);
+    return decode_groups_per_cu<TT, 128, 16>(G);
+  }
+  if (D == 64) return decode_groups_per_cu<TT, 64, 8>(G);
+  if (D == 128) return decode_groups_per_cu<TT, 128, 8>(G);
+  return decode_groups_per_cu<TT, 256, 8>(G);
+}
+
+static int64_t resident_decode_waves(int dtype, int64_t D, int W, int64_t G) {
+  int dev = 0, cus = 0;
+  int per = 0;
+  if (hipGetDevice(&dev) == hipSuccess &&
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess)
+    per = dtype == KVHOT_BF16 ? decode_groups_per_cu<BF16>(D, W, G)
+                              : decode_groups_per_cu<F16>(D, W, G);
+  if (cus <= 0 || per <= 0) {
+    (void)hipGetLastError();
+    return 4096;
+  }
+  return static_cast<int64_t>(cus) * per * W;
+}
+
+struct Piece {
+  int row, kvh, s0, s1, part, seg;
+};
+
+// Minimum slices per decode work-group: below it, a split costs more (partial
+// stores and a merge) than the parallelism gains.
+constexpr int64_t kMinGroupSlicesPerWave = 2;
+// Split pieces shorter than this are not cut off a segment.
+constexpr int64_t kMinPieceSlices = 4;
+// Cost model for choosing a plan that cuts no segment (and so needs no merge
+// launch): the merge launch and its gap cost about kMergeLaunchUs, and a
+// work-group streams K/V at about kDecodeRateGBs / (work-groups) GB/s
+// (measured on MI355X: 5.5-6 TB/s in the decode kernel's steady state).
+constexpr double kMergeLaunchUs = 5.0;
+constexpr double kDecodeRateGBs = 5500.0;
+// Kv heads stream at different rates: which HBM channels a head's rows hit
+// follows from the row's byte offset inside a token's [Hkv, D] row, and on
+// MI355X two of eight 256-byte offsets read about 16% slower in every XCD
+// (shifting the pool by 256 bytes moves the slow heads along).  A work-group
+// of one head's segments then ends late or early with its head; one that
+// holds a mix of heads averages the rates (its waves share the slices).  So
+// the packing below places a segment, among the up to kMixCandidates
+// work-groups within kMixSlack slices of the least loaded, in the one that
+// holds the fewest segments of its kv head.
+constexpr int kMixCandidates = 8;
+constexpr int64_t kMixSlack = 2;
+
+// Decode launch list.  Work-groups of one device-full are given equal numbers
+// of 16-token slices (inside a work-group the waves balance themselves by
+// claiming slices, so only the per-work-group total matters): the (row, kv
+// head) segments are laid end to end and cut every `target` slices, a
+// segment that straddles a cut becoming parts in several work-groups (joined
+// by attn_merge_kernel).  A work-group holds at most W pieces.  Its waves are
+// shared among its pieces in proportion to their slices, and each wave's
+// starting range is an even share of its piece.  With given_pt > 0 segments
+// are first cut at multiples of given_pt keys and those partitions are never
+// split further.  Otherwise, when that plan cuts some segment, the uncut
+// alternative is tried too: whole segments, longest first, each to the
+// least-loaded work-group with a free wave (LPT).  It is taken when its
+// longest work-group holds fewer extra slices than a merge launch costs
+// (slice_bytes per slice at the per-work-group rate).
+//
+// Per wave two int4: (row | parts << 16, kvh | part << 16, first slice, end
+// slice) and (query token, visible keys, physical block of the first slice
+// or -1, partial index).  Per split segment two int4: (query token, kv head,
+// parts, first partial index) and zeros.  Returns false when a count does not
+// fit its 16-bit field.
+static bool plan_decode(const int32_t* q_lens, const int32_t* k_lens, const int32_t* q_offs,
+                        const int32_t* q_starts, const int32_t* bt, int64_t bt_stride, int64_t bs,
+                        int64_t rows, int64_t Hkv, bool causal, int W, int64_t groups,
+                        int64_t given_pt, int64_t slice_bytes, std::vector<int4>& dec,
+                        std::vector<int4>& mrg, int64_t& partials) {
+  dec.clear();
+  mrg.clear();
+  partials = 0;
+  std::vector<int64_t> kend(rows, -1);
+  int64_t total = 0;
+  for (int64_t r = 0; r < rows; ++r) {
+    if (q_lens[r] != 1) continue;
+    const int64_t klen = k_lens[r], off = q_offs[r];
+    kend[r] = std::max<int64_t>(causal ? std::min(klen, off + 1) : klen, 0);
+    total += (kend[r] + 15) / 16 * Hkv;
+  }
+  const int64_t target = std::max<int64_t>((total + std::max<int64_t>(groups, 1) - 1) / std::max<int64_t>(groups, 1),
+                                           kMinGroupSlicesPerWave * W);
+  const int64_t slack = std::max<int64_t>(2, target / 32);
+
+  std::vector<std::vector<Piece>> wgs;
+  std::vector<Piece> cur;
+  int64_t load = 0;
+  auto close = [&]() {
+    if (!cur.empty()) wgs.push_back(cur);
+    cur.clear();
+    load = 0;
+  };
+  std::vector<int> seg_parts;  // parts per segment (row, kv head)
+  std::vector<int> seg_row, seg_kvh;
+  // Adds slices [s, s + rem) of segment seg (row r, kv head h) to the open
+  // work-groups: whole when it is a fixed partition p, else cut at the
+  // work-group loads.
+  auto place = [&](int seg, int64_t r, int64_t h, int64_t s, int64_t rem, int64_t p, bool splittable) {
+    for (;;) {
+      if (static_cast<int>(cur.size()) == W) close();
+      const int64_t space = target - load;
+      if (rem <= space + slack || (!splittable && cur.empty())) {
+        const int part = splittable ? seg_parts[seg]++ : static_cast<int>(p);
+        cur.push_back(Piece{static_cast<int>(r), static_cast<int>(h), static_cast<int>(s),
+                            static_cast<int>(s + rem), part, seg});
+        load += rem;
+        return;
+      }
+      if (!splittable || space < kMinPieceSlices) {
+        close();
+        continue;
+      }
+      int64_t take = space;
+      if (rem - take < kMinPieceSlices) take = rem - kMinPieceSlices;
+      cur.push_back(Piece{static_cast<int>(r), static_cast<int>(h), static_cast<int>(s),
+                          static_cast<int>(s + take), seg_parts[seg]++, seg});
+      s += take;
+      rem -= take;
+      close();
+    }
+  };
+  const int64_t pt_sl = given_pt > 0 ? given_pt / 16 : 0;
+  for (int64_t r = 0; r < rows; ++r) {
+    if (kend[r] < 0) continue;
+    const int64_t n = (kend[r] + 15) / 16;
+    const int seg0 = static_cast<int>(seg_parts.size());
+    for (int64_t h = 0; h < Hkv; ++h) {
+      seg_parts.push_back(0);
+      seg_row.push_back(static_cast<int>(r));
+      seg_kvh.push_back(static_cast<int>(h));
+    }
+    if (pt_sl > 0) {
+      // Fixed partitions, partition-major over the row's kv heads: a
+      // work-group's run of partitions spans the heads, whose streaming
+      // rates differ (see kMixCandidates).
+      const int64_t natoms = std::max<int64_t>((n + pt_sl - 1) / pt_sl, 1);
+      for (int64_t p = 0; p < natoms; ++p) {
+        const int64_t s = p * pt_sl;
+        for (int64_t h = 0; h < Hkv; ++h) place(seg0 + static_cast<int>(h), r, h, s, std::min(n, s + pt_sl) - s, p, false);
+      }
+      for (int64_t h = 0; h < Hkv; ++h) seg_parts[seg0 + h] = static_cast<int>(natoms);
+    } else {
+      for (int64_t h = 0; h < Hkv; ++h) place(seg0 + static_cast<int>(h), r, h, 0, n, 0, true);
+    }
+  }
+  close();
+
+  bool any_cut = false;
+  for (int p : seg_parts) any_cut = any_cut || p > 1;
+  if (given_pt == 0 && any_cut) {
+    const int nseg = static_cast<int>(seg_parts.size());
+    std::vector<int64_t> n(nseg);
+    std::vector<int> order(nseg);
+    for (int sg = 0; sg < nseg; ++sg) {
+      n[sg] = (kend[seg_row[sg]] + 15) / 16;
+      order[sg] = sg;
+    }
+    std::stable_sort(order.begin(), order.end(), [&](int x, int y) { return n[x] > n[y]; });
+    const int64_t ng = std::max<int64_t>(std::max<int64_t>(groups, 1), (nseg + W - 1) / W);
+    // Min-heap of (slices, work-group); a work-group leaves it when full.
+    std::vector<std::pair<int64_t, int64_t>> heap;
+    heap.reserve(ng);
+    for (int64_t g2 = 0; g2 < ng; ++g2) heap.emplace_back(0, g2);
+    std::vector<std::vector<Piece>> lpt(ng);
+    std::vector<int> held(static_cast<size_t>(ng * Hkv), 0);  // segments of each kv head per work-group
+    std::vector<std::pair<int64_t, int64_t>> cand;
+    int64_t lmax = 0;
+    for (int sg : order) {
+      const int h = seg_kvh[sg];
+      cand.clear();
+      std::pop_heap(heap.begin(), heap.end(), std::greater<>());
+      cand.push_back(heap.back());
+      heap.pop_back();
+      while (static_cast<int>(cand.size()) < kMixCandidates && !heap.empty() &&
+             heap.front().first <= cand[0].first + kMixSlack) {
+        std::pop_heap(heap.begin(), heap.end(), std::greater<>());
+        cand.push_back(heap.back());
+        heap.pop_back();
+      }
+      size_t c = 0;
+      for (size_t k = 1; k < cand.size(); ++k)
+        if (held[cand[k].second * Hkv + h] < held[cand[c].second * Hkv + h]) c = k;
+      for (size_t k = 0; k < cand.size(); ++k) {
+        if (k == c) continue;
+        heap.push_back(cand[k]);
+        std::push_heap(heap.begin(), heap.end(), std::greater<>());
+      }
+      auto [ld, g2] = cand[c];
+      lpt[g2].push_back(Piece{seg_row[sg], seg_kvh[sg], 0, static_cast<int>(n[sg]), 0, sg});
+      ++held[g2 * Hkv + h];
+      ld += n[sg];
+      lmax = std::max(lmax, ld);
+      if (static_cast<int>(lpt[g2].size()) < W) {
+        heap.push_back({ld, g2});
+        std::push_heap(heap.begin(), heap.end(), std::greater<>());
+      }
+    }
+    const double slice_us = static_cast<double>(slice_bytes) * ng / (kDecodeRateGBs * 1e3);
+    if (static_cast<double>(lmax - target) * slice_us <= kMergeLaunchUs) {
+      wgs.clear();
+      for (auto& g2 : lpt)
+        if (!g2.empty()) wgs.push_back(std::move(g2));
+      std::fill(seg_parts.begin(), seg_parts.end(), 1);
+    }
+  }
+
+  // Partial indices of split segments.
+  std::vector<int64_t> seg_base(seg_parts.size(), -1);
+  for (size_t sg = 0; sg < seg_parts.size(); ++sg) {
+    if (seg_parts[sg] > 32767) return false;  // bits 16-30 of a wave descriptor's first int
+    if (seg_parts[sg] > 1) {
+      seg_base[sg] = partials;
+      mrg.push_back(int4{q_starts[seg_row[sg]], seg_kvh[sg], seg_parts[sg], static_cast<int>(partials)});
+      mrg.push_back(int4{0, 0, 0, 0});
+      partials += seg_parts[sg];
+      if (partials > 0x7fffffff) return false;
+    }
+  }
+
+  for (const auto& g : wgs) {
+    // Waves per piece: one each, the rest to the piece with most slices per wave.
+    const int k = static_cast<int>(g.size());
+    std::vector<int> w(k, 1);
+    for (int extra = W - k; extra > 0; --extra) {
+      int best = 0;
+      for (int i = 1; i < k; ++i)
+        if (static_cast<int64_t>(g[i].s1 - g[i].s0) * w[best] > static_cast<int64_t>(g[best].s1 - g[best].s0) * w[i])
+          best = i;
+      ++w[best];
+    }
+    for (int i = 0; i < k; ++i) {
+      const Piece& pc = g[i];
+      const int nparts = seg_parts[pc.seg];
+      const int n = pc.s1 - pc.s0;
+      const int r = pc.row;
+      const int pidx = nparts > 1 ? static_cast<int>(seg_base[pc.seg] + pc.part) : 0;
+      for (int j = 0; j < w[i]; ++j) {
+        const int a0 = pc.s0 + static_cast<int>((static_cast<int64_t>(n) * j) / w[i]);
+        const int a1 = pc.s0 + static_cast<int>((static_cast<int64_t>(n) * (j + 1)) / w[i]);
+        const int64_t lb = 16 * static_cast<int64_t>(a0) / bs;
+        const int first = (a0 < a1 && lb < bt_stride) ? bt[r * bt_stride + lb] : -1;
+        dec.push_back(int4{r | (nparts << 16), pc.kvh | (pc.part << 16), a0, a1});
+        dec.push_back(int4{q_starts[r], static_cast<int>(kend[r]), first, pidx});
+      }
+    }
+  }
+  return true;
+}
+
 // Prefill launch list: (row, kv head, query block) units, longest key range first.
 static void plan_prefill(const int32_t* q_lens, const int32_t* k_lens, const int32_t* q_offs,
                          int64_t rows, int64_t Hkv, int64_t G, int64_t D, bool causal,
@@ -2280,13 +1736,15 @@ static void plan_prefill(const int32_t* q_lens, const int32_t* k_lens, const int
 }
 
 template <class TT, int D, int W>
-static void launch_decode(const AttnArgs& a, int64_t rows, hipStream_t stream) {
-  const dim3 grid(static_cast<uint32_t>(a.Hkv), static_cast<uint32_t>(a.max_parts), static_cast<uint32_t>(rows));
+static void launch_decode(const AttnArgs& a, int64_t rows, int64_t n_dec, hipStream_t stream) {
+  dim3 grid = a.sched ? dim3(static_cast<uint32_t>(n_dec / W))
+                      : dim3(static_cast<uint32_t>(a.Hkv), static_cast<uint32_t>(a.max_parts),
+                             static_cast<uint32_t>(rows));
   AttnArgs da = a;
   da.dec_slots = decode_slots(W, a.G, D);
   const size_t lds = static_cast<size_t>(decode_lds_words(W, da.dec_slots, a.G, D) * 4);
-  if (lds > static_cast<size_t>(kDefaultLdsBytes))
-    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(attn_decode_kernel<TT, D, W>),
+  if (lds > kMaxLdsBytes)
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_decode_kernel<TT, D, W>),
                               hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
   hipLaunchKernelGGL((attn_decode_kernel<TT, D, W>), grid, dim3(64 * W), lds, stream, da);
 }
@@ -2333,20 +1791,15 @@ static AuxStream* aux_stream() {
   return &x;
 }
 
-// With a schedule: prefill work-groups (units [0, n_pre)) and the decode
-// launch over dec_groups work-groups (the decode section after them).
-// Without one: the grid-mode decode (plus attn_merge_kernel for rows of
-// several partitions) and prefill over the padded grid.  use_aux: a mixed
-// batch's prefill runs on the device's second stream.
 template <class TT, int D>
-static void launch_mfma(const AttnArgs& a, int waves, int64_t rows, int64_t max_q, int64_t n_pre,
-                        int64_t dec_groups, int64_t dec_lds, bool use_aux, hipStream_t stream) {
-  const bool dec = !a.sched || dec_groups > 0;
+static void launch_mfma(const AttnArgs& a, int waves, int64_t rows, int64_t max_q, int64_t n_dec,
+                        int64_t n_pre, int64_t n_merge, hipStream_t stream) {
+  const bool dec = !a.sched || n_dec > 0;
   const bool pre = a.sched ? n_pre > 0 : max_q >= 2;
   hipStream_t pre_stream = stream;
   std::unique_lock<std::mutex> lock(g_aux_mutex, std::defer_lock);
   AuxStream* aux = nullptr;
-  if (dec && pre && a.sched && use_aux) {
+  if (dec && pre && a.sched) {
     lock.lock();
     aux = aux_stream();
     if (aux && hipEventRecord(aux->fork, stream) == hipSuccess &&
@@ -2363,26 +1816,23 @@ static void launch_mfma(const AttnArgs& a, int waves, int64_t rows, int64_t max_
     const int64_t nqb = (max_q + qpw - 1) / qpw;
     dim3 grid = a.sched ? dim3(static_cast<uint32_t>(n_pre))
                         : dim3(static_cast<uint32_t>(a.Hkv * nqb), 1u, static_cast<uint32_t>(rows));
-    hipLaunchKernelGGL((attn_prefill_kernel<TT, D, NM>), grid, dim3(64 * kPreWaves), 0, pre_stream, a);
+    AttnArgs pa = a;
+    if (a.sched) pa.sched = a.sched + 2 * n_dec;
+    hipLaunchKernelGGL((attn_prefill_kernel<TT, D, NM>), grid, dim3(64 * kPreWaves), 0, pre_stream, pa);
   }
   if (dec) {
-    if (a.sched) {
-      AttnArgs da = a;
-      da.dsched = a.sched + 2 * n_pre;
-      launch_decode2<TT, D>(da, dec_groups, dec_lds, stream);
+    if constexpr (D <= 128) {
+      if (waves == 16)
+        launch_decode<TT, D, 16>(a, rows, n_dec, stream);
+      else
+        launch_decode<TT, D, 8>(a, rows, n_dec, stream);
     } else {
-      if constexpr (D <= 128) {
-        if (waves == 16)
-          launch_decode<TT, D, 16>(a, rows, stream);
-        else
-          launch_decode<TT, D, 8>(a, rows, stream);
-      } else {
-        launch_decode<TT, D, 8>(a, rows, stream);
-      }
-      if (a.max_parts > 1) {
-        const dim3 mgrid(static_cast<uint32_t>((a.Hq * (D / 8) + 63) / 64), static_cast<uint32_t>(rows));
-        hipLaunchKernelGGL((attn_merge_kernel<TT, D>), mgrid, dim3(64), 0, stream, a);
-      }
+      launch_decode<TT, D, 8>(a, rows, n_dec, stream);
+    }
+    if (a.sched ? n_merge > 0 : a.max_parts > 1) {
+      dim3 mgrid = a.sched ? dim3(static_cast<uint32_t>(n_merge))
+                           : dim3(static_cast<uint32_t>((a.Hq * (D / 8) + 63) / 64), static_cast<uint32_t>(rows));
+      hipLaunchKernelGGL((attn_merge_kernel<TT, D>), mgrid, dim3(a.sched ? 64 * kMergeWaves : 64), 0, stream, a);
     }
   }
   if (aux) {
@@ -2392,17 +1842,99 @@ static void launch_mfma(const AttnArgs& a, int waves, int64_t rows, int64_t max_
   }
 }
 
-// kvhot_paged_attention's body.  use_aux: a mixed batch's prefill may run on
-// the device's second stream (created on first use).
-static int paged_attention_impl(
-    const void* q, const int64_t q_strides[3], const void* k_cache, const int64_t k_cache_strides[4],
-    const void* v_cache, const int64_t v_cache_strides[4], void* out, const int64_t out_strides[3], float* lse,
-    const int64_t lse_strides[2], const int32_t* block_table, int64_t bt_row_stride, const int32_t* q_lens,
-    const int32_t* k_lens, const int32_t* q_starts, const int32_t* q_pos_offsets, int64_t num_rows,
-    int64_t total_query, int64_t max_q_len, int64_t max_k_len, int64_t num_q_heads, int64_t num_kv_heads,
-    int64_t head_dim, int64_t block_size, int64_t num_blocks, float scale, int is_causal, int dtype,
-    int64_t partition_tokens, const int32_t* schedule, const int64_t* schedule_info, void* workspace,
-    int64_t workspace_bytes, bool use_aux, void* stream) {
+}  // namespace kvhot
+
+using namespace kvhot;
+
+extern "C" int64_t kvhot_paged_attention_workspace_bytes(
+    int64_t num_rows, int64_t total_query, int64_t max_q_len, int64_t max_k_len,
+    int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim,
+    int64_t block_size, int64_t partition_tokens, int dtype) {
+  (void)total_query;
+  if (num_rows < 0 || max_q_len < 0 || max_k_len < 0 || num_q_heads <= 0 ||
+      num_kv_heads <= 0 || head_dim <= 0 || block_size <= 0 || partition_tokens < 0 ||
+      num_q_heads % num_kv_heads != 0 || dtype_size(dtype) == 0)
+    return KVHOT_EINVAL;
+  const Plan pl = make_plan(num_rows, max_q_len, max_k_len, num_q_heads, num_kv_heads,
+                            head_dim, block_size, partition_tokens, dtype);
+  return pl.grid_ok ? pl.workspace_bytes(num_q_heads / num_kv_heads, head_dim) : 0;
+}
+
+extern "C" int64_t kvhot_paged_attention_schedule(
+    const int32_t* q_lens, const int32_t* k_lens, const int32_t* q_starts,
+    const int32_t* q_pos_offsets, const int32_t* block_table, int64_t bt_row_stride,
+    int64_t num_rows, int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim,
+    int64_t block_size, int64_t partition_tokens, int is_causal, int dtype,
+    int32_t* units, int64_t capacity_units, int64_t* num_decode_units,
+    int64_t* num_prefill_units, int64_t* num_merge_units, int64_t* workspace_bytes) {
+  clear_error();
+  if (num_rows < 0 || num_q_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0 ||
+      block_size <= 0 || partition_tokens < 0 || num_q_heads % num_kv_heads != 0 ||
+      dtype_size(dtype) == 0 || capacity_units < 0 || bt_row_stride < 0)
+    return set_error(KVHOT_EINVAL, "paged_attention_schedule: bad sizes");
+  if (num_rows > 65535 || num_q_heads > 65535)
+    return set_error(KVHOT_EUNSUPPORTED, "paged_attention_schedule: rows or heads too large");
+  if (num_rows > 0 && (!q_lens || !k_lens || !q_starts || !q_pos_offsets ||
+                       (bt_row_stride > 0 && !block_table)))
+    return set_error(KVHOT_EINVAL, "paged_attention_schedule: null host arrays");
+  if (partition_tokens != 0 && (partition_tokens % 32 != 0 || partition_tokens > (1 << 20)))
+    return set_error(KVHOT_EINVAL, "paged_attention_schedule: bad partition_tokens");
+  int64_t max_q = 0, max_k = 0;
+  for (int64_t r = 0; r < num_rows; ++r) {
+    if (q_lens[r] < 0 || k_lens[r] < 0)
+      return set_error(KVHOT_EINVAL, "paged_attention_schedule: negative length");
+    max_q = std::max<int64_t>(max_q, q_lens[r]);
+    max_k = std::max<int64_t>(max_k, k_lens[r]);
+  }
+  std::vector<int4> dec, pre, mrg;
+  int64_t partials = 0;
+  const Plan pl = make_plan(num_rows, max_q, max_k, num_q_heads, num_kv_heads, head_dim,
+                            block_size, partition_tokens, dtype);
+  if (pl.mfma) {
+    const int64_t G = num_q_heads / num_kv_heads;
+    const int64_t groups = resident_decode_waves(dtype, head_dim, pl.waves, G) / pl.waves;
+    if (plan_decode(q_lens, k_lens, q_pos_offsets, q_starts, block_table, bt_row_stride, block_size,
+                    num_rows, num_kv_heads, is_causal != 0, pl.waves, groups, partition_tokens,
+                    32 * head_dim * dtype_size(dtype), dec, mrg, partials)) {
+      plan_prefill(q_lens, k_lens, q_pos_offsets, num_rows, num_kv_heads, G, head_dim,
+                   is_causal != 0, pre);
+    } else {  // counts beyond the descriptor fields: no schedule
+      dec.clear();
+      mrg.clear();
+      partials = 0;
+    }
+  }
+  // Units are 8 int32 (two int4) each: decode waves, prefill work-groups,
+  // merge units.
+  const int64_t n_dec = static_cast<int64_t>(dec.size() / 2);
+  const int64_t n_pre = static_cast<int64_t>(pre.size() / 2);
+  const int64_t n_mrg = static_cast<int64_t>(mrg.size() / 2);
+  if (num_decode_units) *num_decode_units = n_dec;
+  if (num_prefill_units) *num_prefill_units = n_pre;
+  if (num_merge_units) *num_merge_units = n_mrg;
+  if (workspace_bytes) *workspace_bytes = partials * partial_bytes(num_q_heads / num_kv_heads, head_dim);
+  if (units && capacity_units >= n_dec + n_pre + n_mrg) {
+    int4* out = reinterpret_cast<int4*>(units);
+    std::copy(dec.begin(), dec.end(), out);
+    std::copy(pre.begin(), pre.end(), out + dec.size());
+    std::copy(mrg.begin(), mrg.end(), out + dec.size() + pre.size());
+  }
+  return n_dec + n_pre + n_mrg;
+}
+
+extern "C" int kvhot_paged_attention(
+    const void* q, const int64_t q_strides[3], const void* k_cache,
+    const int64_t k_cache_strides[4], const void* v_cache,
+    const int64_t v_cache_strides[4], void* out, const int64_t out_strides[3],
+    float* lse, const int64_t lse_strides[2], const int32_t* block_table,
+    int64_t bt_row_stride, const int32_t* q_lens, const int32_t* k_lens,
+    const int32_t* q_starts, const int32_t* q_pos_offsets, int64_t num_rows,
+    int64_t total_query, int64_t max_q_len, int64_t max_k_len,
+    int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim,
+    int64_t block_size, int64_t num_blocks, float scale, int is_causal,
+    int dtype, int64_t partition_tokens, const int32_t* schedule,
+    int64_t num_decode_units, int64_t num_prefill_units, int64_t num_merge_units,
+    int64_t schedule_workspace_bytes, void* workspace, int64_t workspace_bytes, void* stream) {
   clear_error();
   const int64_t es = dtype_size(dtype);
   if (es == 0) return set_error(KVHOT_EINVAL, "paged_attention: bad dtype");
@@ -2412,8 +1944,6 @@ static int paged_attention_impl(
     return set_error(KVHOT_EINVAL, "paged_attention: bad sizes");
   if (num_q_heads % num_kv_heads != 0)
     return set_error(KVHOT_EINVAL, "paged_attention: num_q_heads % num_kv_heads != 0");
-  if (schedule && !schedule_info)
-    return set_error(KVHOT_EINVAL, "paged_attention: a schedule needs its schedule_info");
   if (num_rows == 0 || total_query == 0 || max_q_len == 0) return 0;
   if (!q || !k_cache || !v_cache || !out || !q_lens || !k_lens || !q_starts ||
       !q_pos_offsets || !q_strides || !k_cache_strides || !v_cache_strides ||
@@ -2431,21 +1961,6 @@ static int paged_attention_impl(
       (partition_tokens % 32 != 0 || partition_tokens > (1 << 20)))
     return set_error(KVHOT_EINVAL,
                      "paged_attention: partition_tokens must be a multiple of 32 and <= 2^20");
-  int64_t n_pre = 0, n_dec = 0, dec_groups = 0, sched_ws = 0, dec_lds = 0, dec_banks = 0;
-  if (schedule) {
-    const int64_t* si = schedule_info;
-    n_pre = si[KVHOT_SCHED_PREFILL_UNITS];
-    n_dec = si[KVHOT_SCHED_DECODE_UNITS];
-    dec_groups = si[KVHOT_SCHED_DECODE_GROUPS];
-    sched_ws = si[KVHOT_SCHED_WORKSPACE_BYTES];
-    dec_lds = si[KVHOT_SCHED_DECODE_LDS_BYTES];
-    dec_banks = si[KVHOT_SCHED_DECODE_BANKS];
-    if (n_pre < 0 || n_dec < 0 || dec_groups < 0 || sched_ws < 0 || si[KVHOT_SCHED_UNITS] != n_pre + n_dec ||
-        n_pre > 0x7fffffff || dec_groups > 0x7fffffff || (n_dec > 0) != (dec_groups > 0) ||
-        (n_dec > 0 && (n_dec < 1 + dec_groups || dec_lds <= 0 || dec_lds > 160 * 1024 ||
-                       ((dec_banks & 255) != 4 && (dec_banks & 255) != 8) || (dec_banks & ~511) != 0)))
-      return set_error(KVHOT_EINVAL, "paged_attention: schedule_info does not describe a launch list");
-  }
 
   AttnArgs a{};
   a.q = q; a.q_st = q_strides[0]; a.q_sh = q_strides[1];
@@ -2466,17 +1981,22 @@ static int paged_attention_impl(
   a.causal = is_causal ? 1 : 0;
   a.D = static_cast<int32_t>(head_dim);
   a.total_q = total_query;
+  const int64_t n_dec = schedule ? num_decode_units : 0;
+  const int64_t n_pre = schedule ? num_prefill_units : 0;
+  const int64_t n_mrg = schedule ? num_merge_units : 0;
+  if (schedule && (n_dec < 0 || n_pre < 0 || n_mrg < 0 || n_dec > 0x7fffffff ||
+                   n_pre > 0x7fffffff || n_mrg > 0x7fffffff || schedule_workspace_bytes < 0))
+    return set_error(KVHOT_EINVAL, "paged_attention: bad schedule unit counts");
   a.sched = reinterpret_cast<const int4*>(schedule);
-  a.dec_banks = static_cast<int32_t>(dec_banks & 255);
-  a.dec_slot_mode = (dec_banks & 256) ? 1 : 0;
+  a.merge_units = (schedule && n_mrg > 0) ? a.sched + 2 * (n_dec + n_pre) : nullptr;
   a.max_parts = 1;
   hipStream_t s = static_cast<hipStream_t>(stream);
 
   Plan pl = make_plan(num_rows, max_q_len, max_k_len, num_q_heads, num_kv_heads, head_dim,
                       block_size, partition_tokens, dtype);
-  if (schedule && !pl.mfma && (n_pre > 0 || n_dec > 0))
-    return set_error(KVHOT_EINVAL, "paged_attention: the schedule does not match this shape or dtype");
   if (!schedule && !pl.grid_ok) pl.mfma = false;
+  if (schedule && pl.mfma && n_dec % pl.waves != 0)
+    return set_error(KVHOT_EINVAL, "paged_attention: decode schedule is not whole work-groups");
   if (pl.mfma) {
     // 16-byte vector loads/stores need 16-byte aligned rows.
     const int64_t al = 16 / es;
@@ -2490,33 +2010,26 @@ static int paged_attention_impl(
     // inside it) must fit their 32-bit ranges.
     const bool fits = a.k_sb > 0 && a.v_sb > 0 && es * a.k_sb < (1LL << 31) && es * a.v_sb < (1LL << 31) &&
                       a.k_st > 0 && a.v_st > 0 && 16 * es * a.k_st < (1LL << 31) && 16 * es * a.v_st < (1LL << 31);
-    if (!aligned || !fits) {
-      if (schedule && (n_pre > 0 || n_dec > 0))
-        return set_error(KVHOT_EUNSUPPORTED,
-                         "paged_attention: a schedule needs 16-byte aligned rows and block strides below 2 GiB");
-      pl.mfma = false;
-    }
+    if (!aligned || !fits) pl.mfma = false;
   }
   if (pl.mfma) {
     const int64_t pb = partial_bytes(a.G, head_dim);
-    const int64_t need = schedule ? sched_ws : pl.workspace_bytes(a.G, head_dim);
+    if (schedule && n_mrg > 0 && schedule_workspace_bytes < pb)
+      return set_error(KVHOT_EINVAL, "paged_attention: a schedule with merge units needs partials");
+    const int64_t need = schedule ? (n_mrg > 0 ? schedule_workspace_bytes : 0) : pl.workspace_bytes(a.G, head_dim);
     if (need > 0) {
       if (!workspace || workspace_bytes < need)
         return set_error(KVHOT_EWORKSPACE,
                          "paged_attention: workspace of " + std::to_string(need) + " bytes required");
-      if (need - kCounterBytes >= (1LL << 31))
-        return set_error(KVHOT_EUNSUPPORTED, "paged_attention: split-K partials beyond 2 GiB");
-      a.num_partials = (need - kCounterBytes) / pb;
-      a.merge_ctr = static_cast<int*>(workspace);
-      a.ws_o = reinterpret_cast<float*>(static_cast<char*>(workspace) + kCounterBytes);
+      a.num_partials = schedule ? workspace_bytes / pb : pl.partials;
+      a.ws_o = static_cast<float*>(workspace);
       a.ws_lse = a.ws_o + a.num_partials * a.G * head_dim;
     }
     if (!schedule) {
       a.part_tokens = pl.part_tokens;
       a.max_parts = pl.max_parts;
     }
-#define KVHOT_MFMA(TT, DD) \
-  launch_mfma<TT, DD>(a, pl.waves, num_rows, max_q_len, n_pre, dec_groups, dec_lds, use_aux, s)
+#define KVHOT_MFMA(TT, DD) launch_mfma<TT, DD>(a, pl.waves, num_rows, max_q_len, n_dec, n_pre, n_mrg, s)
     if (dtype == KVHOT_BF16) {
       if (head_dim == 64) KVHOT_MFMA(BF16, 64);
       else if (head_dim == 128) KVHOT_MFMA(BF16, 128);
@@ -2541,105 +2054,4 @@ static int paged_attention_impl(
   else
     hipLaunchKernelGGL(attn_generic_kernel<F16>, grid, dim3(64), 0, s, a);
   return launch_status("paged_attention");
-}
-
-}  // namespace kvhot
-
-
-using namespace kvhot;
-
-extern "C" int64_t kvhot_paged_attention_workspace_bytes(
-    int64_t num_rows, int64_t total_query, int64_t max_q_len, int64_t max_k_len,
-    int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim,
-    int64_t block_size, int64_t partition_tokens, int dtype) {
-  (void)total_query;
-  if (num_rows < 0 || max_q_len < 0 || max_k_len < 0 || num_q_heads <= 0 ||
-      num_kv_heads <= 0 || head_dim <= 0 || block_size <= 0 || partition_tokens < 0 ||
-      num_q_heads % num_kv_heads != 0 || dtype_size(dtype) == 0)
-    return KVHOT_EINVAL;
-  const Plan pl = make_plan(num_rows, max_q_len, max_k_len, num_q_heads, num_kv_heads,
-                            head_dim, block_size, partition_tokens, dtype);
-  return pl.grid_ok ? pl.workspace_bytes(num_q_heads / num_kv_heads, head_dim) : 0;
-}
-
-extern "C" int64_t kvhot_paged_attention_schedule(
-    const int32_t* q_lens, const int32_t* k_lens, const int32_t* q_starts,
-    const int32_t* q_pos_offsets, int64_t num_rows, int64_t num_q_heads,
-    int64_t num_kv_heads, int64_t head_dim, int64_t block_size,
-    int64_t partition_tokens, int is_causal, int dtype, int32_t* units,
-    int64_t capacity_units, int64_t* info) {
-  clear_error();
-  if (num_rows < 0 || num_q_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0 ||
-      block_size <= 0 || partition_tokens < 0 || num_q_heads % num_kv_heads != 0 ||
-      dtype_size(dtype) == 0 || capacity_units < 0)
-    return set_error(KVHOT_EINVAL, "paged_attention_schedule: bad sizes");
-  if (num_rows > 65535 || num_q_heads > 65535)
-    return set_error(KVHOT_EUNSUPPORTED, "paged_attention_schedule: rows or heads too large");
-  if (num_rows > 0 && (!q_lens || !k_lens || !q_starts || !q_pos_offsets))
-    return set_error(KVHOT_EINVAL, "paged_attention_schedule: null host arrays");
-  if (partition_tokens != 0 && (partition_tokens % 32 != 0 || partition_tokens > (1 << 20)))
-    return set_error(KVHOT_EINVAL, "paged_attention_schedule: bad partition_tokens");
-  int64_t max_q = 0, max_k = 0;
-  for (int64_t r = 0; r < num_rows; ++r) {
-    if (q_lens[r] < 0 || k_lens[r] < 0)
-      return set_error(KVHOT_EINVAL, "paged_attention_schedule: negative length");
-    max_q = std::max<int64_t>(max_q, q_lens[r]);
-    max_k = std::max<int64_t>(max_k, k_lens[r]);
-  }
-  const int64_t G = num_q_heads / num_kv_heads;
-  std::vector<int4> pre;
-  DecodePlan dp;
-  const Plan pl = make_plan(num_rows, max_q, max_k, num_q_heads, num_kv_heads, head_dim,
-                            block_size, partition_tokens, dtype);
-  if (pl.mfma) {
-    const int64_t resident = dtype == KVHOT_BF16 ? resident_decode2_groups<BF16>(head_dim)
-                                                 : resident_decode2_groups<F16>(head_dim);
-    if (plan_decode2(q_lens, k_lens, q_pos_offsets, q_starts, num_rows, num_kv_heads, G, head_dim, is_causal != 0,
-                     resident, partition_tokens, dp)) {
-      plan_prefill(q_lens, k_lens, q_pos_offsets, num_rows, num_kv_heads, G, head_dim, is_causal != 0, pre);
-    } else {  // counts beyond the list's fields: no schedule
-      dp = DecodePlan{};
-    }
-  }
-  // Units are 8 int32 (two int4) each: prefill work-groups, then the decode section.
-  const int64_t n_pre = static_cast<int64_t>(pre.size() / 2);
-  const int64_t n_dec = static_cast<int64_t>(dp.units.size() / 2);
-  const int64_t ws = dp.cut_rows > 0 ? kCounterBytes + dp.row_partials * num_kv_heads * partial_bytes(G, head_dim) : 0;
-  if (info) {
-    for (int i = 0; i < KVHOT_SCHED_INFO_LEN; ++i) info[i] = 0;
-    info[KVHOT_SCHED_UNITS] = n_pre + n_dec;
-    info[KVHOT_SCHED_PREFILL_UNITS] = n_pre;
-    info[KVHOT_SCHED_DECODE_UNITS] = n_dec;
-    info[KVHOT_SCHED_DECODE_GROUPS] = dp.groups;
-    info[KVHOT_SCHED_WORKSPACE_BYTES] = ws;
-    info[KVHOT_SCHED_CUT_ROWS] = dp.cut_rows;
-    info[KVHOT_SCHED_DECODE_LDS_BYTES] = dp.lds_bytes;
-    info[KVHOT_SCHED_DECODE_BANKS] = dp.banks;
-  }
-  if (units && capacity_units >= n_pre + n_dec) {
-    int4* out = reinterpret_cast<int4*>(units);
-    std::copy(pre.begin(), pre.end(), out);
-    std::copy(dp.units.begin(), dp.units.end(), out + pre.size());
-  }
-  return n_pre + n_dec;
-}
-
-extern "C" int kvhot_paged_attention(
-    const void* q, const int64_t q_strides[3], const void* k_cache,
-    const int64_t k_cache_strides[4], const void* v_cache,
-    const int64_t v_cache_strides[4], void* out, const int64_t out_strides[3],
-    float* lse, const int64_t lse_strides[2], const int32_t* block_table,
-    int64_t bt_row_stride, const int32_t* q_lens, const int32_t* k_lens,
-    const int32_t* q_starts, const int32_t* q_pos_offsets, int64_t num_rows,
-    int64_t total_query, int64_t max_q_len, int64_t max_k_len,
-    int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim,
-    int64_t block_size, int64_t num_blocks, float scale, int is_causal,
-    int dtype, int64_t partition_tokens, const int32_t* schedule,
-    const int64_t* schedule_info, void* workspace, int64_t workspace_bytes, void* stream) {
-  return kvhot::paged_attention_impl(q, q_strides, k_cache, k_cache_strides, v_cache, v_cache_strides, out,
-                                     out_strides, lse, lse_strides, block_table, bt_row_stride, q_lens, k_lens,
-                                     q_starts, q_pos_offsets, num_rows, total_query, max_q_len, max_k_len,
-                                     num_q_heads, num_kv_heads, head_dim, block_size, num_blocks, scale,
-                                     is_causal, dtype, partition_tokens, schedule, schedule_info, workspace,
-                                     workspace_bytes, true, stream);
 }

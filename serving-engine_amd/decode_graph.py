@@ -26,7 +26,7 @@ import torch
 
 from . import _lib
 from .block import BLOCK_SIZE
-from .paged_attention_kernel import build_slot_mapping, plan_schedule, schedule_key
+from .paged_attention_kernel import build_slot_mapping, schedule_key
 
 
 class DecodeStepGraph:
@@ -106,13 +106,23 @@ class DecodeStepGraph:
 
     def _plan(self, a):
         """Launch list of the step's attention calls from the host arrays."""
-        r = self.r
+        r, mb = self.r, self.max_blocks
         hq, hkv, d, bs, pt, causal, dt = self.shape
-        units, info = plan_schedule(a[0:r], a[r:2 * r], a[2 * r:3 * r], a[3 * r:4 * r], hq, hkv, d, bs, pt,
-                                    causal, dt)
-        if units is None:  # a decode batch of MFMA shapes always has one
-            raise RuntimeError("kvhot_paged_attention_schedule returned no launch list for a decode step")
-        return units, tuple(int(x) for x in info)
+        lib = _lib.load()
+        cnt = [ctypes.c_int64(0) for _ in range(4)]
+        outs = tuple(ctypes.byref(c) for c in cnt)
+        base = a.ctypes.data  # q_lens, k_lens, q_starts, q_pos_offsets, block table: int32 views of `a`
+        args = (base, base + 4 * r, base + 8 * r, base + 12 * r, base + 16 * r, mb, r, hq, hkv, d, bs, pt,
+                1 if causal else 0, dt)
+        total = lib.kvhot_paged_attention_schedule(*args, None, 0, *outs)
+        if total < 0:
+            _lib.check(int(total), "kvhot_paged_attention_schedule")
+        units = torch.empty((max(int(total), 1), 8), dtype=torch.int32, pin_memory=True)
+        if total > 0:
+            got = lib.kvhot_paged_attention_schedule(*args, units.data_ptr(), total, *outs)
+            if got != total:
+                _lib.check(-1 if got >= 0 else int(got), "kvhot_paged_attention_schedule")
+        return units, tuple(int(c.value) for c in cnt)
 
     # -- the recorded step -------------------------------------------------
 
@@ -126,12 +136,13 @@ class DecodeStepGraph:
         self.tokens.copy_(self.logits.argmax(-1))
 
     def _record(self, units, counts):
+        n_dec, n_pre, n_mrg, need = counts
         self._units_dev = units.to(self.device, non_blocking=True)
-        info = (ctypes.c_int64 * len(counts))(*counts)
         # The attention calls find their launch list here (no host copies
         # are read once it is present).
         self.meta["host_q_lens"] = self._host[0].numpy()[: self.r]
-        self.meta["_schedules"] = {schedule_key(self.device, *self.shape): (self._units_dev, info)}
+        self.meta["_schedules"] = {
+            schedule_key(self.device, *self.shape): (self._units_dev, n_dec, n_pre, n_mrg, need)}
         stream = torch.cuda.current_stream(self.device)
         saved = self.tokens.clone()
         # One eager pass on a side stream first (lazy library set-up and

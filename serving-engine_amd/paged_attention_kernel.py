@@ -46,15 +46,12 @@ _WORKSPACES: dict[tuple[int, int], torch.Tensor] = {}
 
 
 def _workspace(device: torch.device, stream: int, nbytes: int) -> torch.Tensor | None:
-    """A workspace of at least nbytes for calls on (device, stream), zero-filled
-    when allocated: its first WORKSPACE_COUNTER_BYTES are counters that must
-    start at zero (every call leaves them zero)."""
     if nbytes <= 0:
         return None
     key = (device.index if device.index is not None else torch.cuda.current_device(), stream)
     ws = _WORKSPACES.get(key)
     if ws is None or ws.numel() < nbytes:
-        ws = torch.zeros(int(nbytes), dtype=torch.uint8, device=device)
+        ws = torch.empty(int(nbytes), dtype=torch.uint8, device=device)
         _WORKSPACES[key] = ws
     return ws
 
@@ -66,32 +63,11 @@ def schedule_key(device, hq, hkv, d, bs, pt, causal, dtype):
     return (hq, hkv, d, bs, pt, bool(causal), dtype, str(device))
 
 
-def plan_schedule(host_q_lens, host_k_lens, host_q_starts, host_q_pos_offsets, hq, hkv, d, bs, pt, causal,
-                  dtype):
-    """Host launch list of kvhot_paged_attention_schedule: (units, info) with
-    units a pinned int32 [n, 8] tensor (None when the call takes no schedule)
-    and info its int64 description (ctypes array of SCHED_INFO_LEN)."""
-    lib = _lib.load()
-    info = (ctypes.c_int64 * _lib.SCHED_INFO_LEN)()
-    args = (host_q_lens.ctypes.data, host_k_lens.ctypes.data, host_q_starts.ctypes.data,
-            host_q_pos_offsets.ctypes.data, len(host_q_lens), hq, hkv, d, bs, pt, 1 if causal else 0, dtype)
-    total = lib.kvhot_paged_attention_schedule(*args, None, 0, info)
-    if total < 0:
-        _lib.check(int(total), "kvhot_paged_attention_schedule")
-    if total == 0:
-        return None, info
-    units = torch.empty((total, 8), dtype=torch.int32, pin_memory=True)
-    got = lib.kvhot_paged_attention_schedule(*args, units.data_ptr(), total, info)
-    if got != total:
-        _lib.check(-1 if got >= 0 else int(got), "kvhot_paged_attention_schedule")
-    return units, info
-
-
 def _schedule(metadata, device, hq, hkv, d, bs, pt, causal, dtype):
-    """(device units, schedule info) of kvhot_paged_attention_schedule for
-    this step, built once per attention shape from the host copies of the
-    metadata and cached in the metadata dict; None without host copies or
-    when the call takes no schedule."""
+    """(device units, n_decode, n_prefill, n_merge, workspace bytes) of
+    kvhot_paged_attention_schedule for this step, built once per attention
+    shape from the host copies of the metadata and cached in the metadata
+    dict; None without host copies."""
     host_q = metadata.get("host_q_lens")
     if host_q is None:
         return None
@@ -99,9 +75,27 @@ def _schedule(metadata, device, hq, hkv, d, bs, pt, causal, dtype):
     cache = metadata.setdefault("_schedules", {})
     if key in cache:
         return cache[key]
-    units, info = plan_schedule(host_q, metadata["host_k_lens"], metadata["host_q_starts"],
-                                metadata["host_q_pos_offsets"], hq, hkv, d, bs, pt, causal, dtype)
-    hit = None if units is None else (units.to(device, non_blocking=True), info)
+    host_k = metadata["host_k_lens"]
+    host_off = metadata["host_q_pos_offsets"]
+    host_qs = metadata["host_q_starts"]
+    host_bt = metadata["host_block_table"]
+    lib = _lib.load()
+    counts = [ctypes.c_int64(0) for _ in range(4)]  # decode, prefill, merge units; workspace bytes
+    args = (host_q.ctypes.data, host_k.ctypes.data, host_qs.ctypes.data, host_off.ctypes.data,
+            host_bt.ctypes.data if host_bt.size else None, host_bt.shape[1] if host_bt.ndim == 2 else 0,
+            len(host_q), hq, hkv, d, bs, pt, 1 if causal else 0, dtype)
+    outs = tuple(ctypes.byref(c) for c in counts)
+    total = lib.kvhot_paged_attention_schedule(*args, None, 0, *outs)
+    if total < 0:
+        _lib.check(int(total), "kvhot_paged_attention_schedule")
+    if total == 0:
+        hit = None
+    else:
+        units = torch.empty((total, 8), dtype=torch.int32, pin_memory=True)
+        got = lib.kvhot_paged_attention_schedule(*args, units.data_ptr(), total, *outs)
+        if got != total:
+            _lib.check(-1 if got >= 0 else int(got), "kvhot_paged_attention_schedule")
+        hit = (units.to(device, non_blocking=True),) + tuple(int(c.value) for c in counts)
     cache[key] = hit
     return hit
 
@@ -176,10 +170,9 @@ def paged_flash_attention(q, k_cache, v_cache, metadata, num_q_heads, num_kv_hea
     plan = _schedule(metadata, device, num_q_heads, num_kv_heads, head_dim, block_size, pt,
                      is_causal, dtype)
     if plan is not None:
-        sched, info = plan
-        need = int(info[_lib.SCHED_WORKSPACE_BYTES])
+        sched, n_dec, n_pre, n_mrg, need = plan
     else:
-        sched, info = None, None
+        sched, n_dec, n_pre, n_mrg = None, 0, 0, 0
         need = lib.kvhot_paged_attention_workspace_bytes(
             num_rows, total_query, max_q, max_k, num_q_heads, num_kv_heads, head_dim,
             block_size, pt, dtype)
@@ -197,7 +190,8 @@ def paged_flash_attention(q, k_cache, v_cache, metadata, num_q_heads, num_kv_hea
         metadata["q_starts"].data_ptr(), metadata["q_pos_offsets"].data_ptr(),
         num_rows, total_query, max_q, max_k, num_q_heads, num_kv_heads, head_dim,
         block_size, num_blocks, float(scale), 1 if is_causal else 0, dtype, pt,
-        sched.data_ptr() if sched is not None else None, info,
+        sched.data_ptr() if sched is not None else None, n_dec, n_pre, n_mrg,
+        need if sched is not None else 0,
         ws.data_ptr() if ws is not None else None, ws.numel() if ws is not None else 0,
         stream)
     _lib.check(status, "kvhot_paged_attention")

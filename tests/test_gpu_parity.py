@@ -308,7 +308,7 @@ def test_config4_prefix_sharing_and_cow(cuda, sea, wl):
     cache = sea._PagedKVCache(T.kv_cache)
     cache.copy_blocks(w.copy_src, w.copy_dst)
     meta = wl.metadata_tensors(w, cuda)
-    bt, host_bt = meta["block_table"], meta["host_block_table"]  # host copy kept equal to the device table
+    bt, host_bt = meta["block_table"], meta["host_block_table"]  # the schedule reads the host copy
     for i, x in enumerate(w.rows):
         bt[i, math.ceil(x.k_len / 16) - 1] = int(w.copy_dst[i])
         host_bt[i, math.ceil(x.k_len / 16) - 1] = int(w.copy_dst[i])
@@ -359,15 +359,25 @@ SHAPES = [
 ]
 
 
+def mfma_shape(hq, hkv, d, dtype):
+    """Shapes the MFMA kernels take: bf16/fp16, head_dim 64/128/256, query
+    groups of 1 to 16 heads (powers of two); the rest run the VALU kernel."""
+    return dtype in (torch.bfloat16, torch.float16) and d in (64, 128, 256) and hq // hkv in (1, 2, 4, 8, 16)
+
+
 @pytest.mark.parametrize("hq,hkv,d,dtype", SHAPES)
 def test_shapes_mixed_batch(cuda, sea, wl, hq, hkv, d, dtype):
     w = custom(wl, MIXED, hq, hkv, d, dtype)
     announce(f"mixed batch Hq={hq} Hkv={hkv} D={d} {dtype}")
     T = wl.make_tensors(w, cuda)
     ref_o, ref_l = oracle_step(w, T)
-    o, l = hip_step(sea, wl, w, T, partition_tokens=64)
+    meta = wl.metadata_tensors(w, T.q.device)
+    o, l = hip_step(sea, wl, w, T, partition_tokens=64, meta=meta)
     live = [i for i, x in enumerate(w.rows) if x.q_len > 0]
     assert_attention(w, o, l, ref_o, ref_l, rows=live)
+    # the path that ran: a launch list (MFMA kernels) exactly for the MFMA shapes
+    plans = [p for p in meta.get("_schedules", {}).values() if p is not None]
+    assert bool(plans) == mfma_shape(hq, hkv, d, dtype), (hq, hkv, d, dtype)
 
 
 def test_non_causal(cuda, sea, wl):
