@@ -209,6 +209,43 @@ int kvhot_paged_attention(
     void* workspace, int64_t workspace_bytes,
     void* stream);
 
+/* Bytes of split-K partials kvhot_paged_attention_noalloc can hold (32 MiB). */
+#define KVHOT_NOALLOC_SCRATCH_BYTES (32LL << 20)
+
+/*
+ * kvhot_paged_attention for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc); it has no counterpart in the reference.  Same arguments and
+ * results as kvhot_paged_attention, without workspace / workspace_bytes: the
+ * split-K partials go to a device-global array of
+ * KVHOT_NOALLOC_SCRATCH_BYTES, one on each device the library runs on, held
+ * until the process ends.  A call that needs more (the schedule's
+ * schedule_workspace_bytes, or kvhot_paged_attention_workspace_bytes without
+ * a schedule) fails with KVHOT_EWORKSPACE before any launch.  Allocates
+ * nothing: no device memory, and no stream or event (a mixed batch's prefill
+ * and decode launches both go to the caller's stream).  Every call on a
+ * device shares that device's array, so calls that overlap on one device (on
+ * different streams, or from threads without ordering) race; calls ordered
+ * on one stream do not.  A call writes every partial it reads, so nothing
+ * needs clearing between calls.
+ */
+int kvhot_paged_attention_noalloc(
+    const void* q, const int64_t q_strides[3],
+    const void* k_cache, const int64_t k_cache_strides[4],
+    const void* v_cache, const int64_t v_cache_strides[4],
+    void* out, const int64_t out_strides[3],
+    float* lse, const int64_t lse_strides[2],
+    const int32_t* block_table, int64_t bt_row_stride,
+    const int32_t* q_lens, const int32_t* k_lens, const int32_t* q_starts,
+    const int32_t* q_pos_offsets, int64_t num_rows, int64_t total_query,
+    int64_t max_q_len, int64_t max_k_len, int64_t num_q_heads,
+    int64_t num_kv_heads, int64_t head_dim, int64_t block_size,
+    int64_t num_blocks, float scale, int is_causal, int dtype,
+    int64_t partition_tokens, const int32_t* schedule,
+    int64_t num_decode_units, int64_t num_prefill_units,
+    int64_t num_merge_units, int64_t schedule_workspace_bytes,
+    void* stream);
+
 #ifdef __cplusplus
 }
 #endif

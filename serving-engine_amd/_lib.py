@@ -23,6 +23,9 @@ KVHOT_F32 = 0
 KVHOT_F16 = 1
 KVHOT_BF16 = 2
 
+# Split-K partials kvhot_paged_attention_noalloc holds (KVHOT_NOALLOC_SCRATCH_BYTES).
+NOALLOC_SCRATCH_BYTES = 32 << 20
+
 _DTYPE_CODES = {
     torch.float32: KVHOT_F32,
     torch.float16: KVHOT_F16,
@@ -66,6 +69,13 @@ SIGNATURES = {
          _vp, _i64, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64,
          _i64, _i64, _i64, _i64, ctypes.c_float, _int, _int, _i64, _vp, _i64, _i64, _i64, _i64,
          _vp, _i64, _vp],
+    ),
+    "kvhot_paged_attention_noalloc": (
+        _int,
+        [_vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p,
+         _vp, _i64, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64,
+         _i64, _i64, _i64, _i64, ctypes.c_float, _int, _int, _i64, _vp, _i64, _i64, _i64, _i64,
+         _vp],
     ),
 }
 

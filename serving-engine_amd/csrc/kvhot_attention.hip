@@ -1793,13 +1793,13 @@ static AuxStream* aux_stream() {
 
 template <class TT, int D>
 static void launch_mfma(const AttnArgs& a, int waves, int64_t rows, int64_t max_q, int64_t n_dec,
-                        int64_t n_pre, int64_t n_merge, hipStream_t stream) {
+                        int64_t n_pre, int64_t n_merge, bool use_aux, hipStream_t stream) {
   const bool dec = !a.sched || n_dec > 0;
   const bool pre = a.sched ? n_pre > 0 : max_q >= 2;
   hipStream_t pre_stream = stream;
   std::unique_lock<std::mutex> lock(g_aux_mutex, std::defer_lock);
   AuxStream* aux = nullptr;
-  if (dec && pre && a.sched) {
+  if (dec && pre && a.sched && use_aux) {
     lock.lock();
     aux = aux_stream();
     if (aux && hipEventRecord(aux->fork, stream) == hipSuccess &&
@@ -1922,7 +1922,9 @@ extern "C" int64_t kvhot_paged_attention_schedule(
   return n_dec + n_pre + n_mrg;
 }
 
-extern "C" int kvhot_paged_attention(
+// kvhot_paged_attention's body.  use_aux: a mixed batch's prefill may run on
+// the device's second stream (created on first use).
+static int paged_attention_impl(
     const void* q, const int64_t q_strides[3], const void* k_cache,
     const int64_t k_cache_strides[4], const void* v_cache,
     const int64_t v_cache_strides[4], void* out, const int64_t out_strides[3],
@@ -1934,7 +1936,8 @@ extern "C" int kvhot_paged_attention(
     int64_t block_size, int64_t num_blocks, float scale, int is_causal,
     int dtype, int64_t partition_tokens, const int32_t* schedule,
     int64_t num_decode_units, int64_t num_prefill_units, int64_t num_merge_units,
-    int64_t schedule_workspace_bytes, void* workspace, int64_t workspace_bytes, void* stream) {
+    int64_t schedule_workspace_bytes, void* workspace, int64_t workspace_bytes, bool use_aux,
+    void* stream) {
   clear_error();
   const int64_t es = dtype_size(dtype);
   if (es == 0) return set_error(KVHOT_EINVAL, "paged_attention: bad dtype");
@@ -2029,7 +2032,7 @@ extern "C" int kvhot_paged_attention(
       a.part_tokens = pl.part_tokens;
       a.max_parts = pl.max_parts;
     }
-#define KVHOT_MFMA(TT, DD) launch_mfma<TT, DD>(a, pl.waves, num_rows, max_q_len, n_dec, n_pre, n_mrg, s)
+#define KVHOT_MFMA(TT, DD) launch_mfma<TT, DD>(a, pl.waves, num_rows, max_q_len, n_dec, n_pre, n_mrg, use_aux, s)
     if (dtype == KVHOT_BF16) {
       if (head_dim == 64) KVHOT_MFMA(BF16, 64);
       else if (head_dim == 128) KVHOT_MFMA(BF16, 128);
@@ -2054,4 +2057,101 @@ extern "C" int kvhot_paged_attention(
   else
     hipLaunchKernelGGL(attn_generic_kernel<F16>, grid, dim3(64), 0, s, a);
   return launch_status("paged_attention");
+}
+
+extern "C" int kvhot_paged_attention(
+    const void* q, const int64_t q_strides[3], const void* k_cache,
+    const int64_t k_cache_strides[4], const void* v_cache,
+    const int64_t v_cache_strides[4], void* out, const int64_t out_strides[3],
+    float* lse, const int64_t lse_strides[2], const int32_t* block_table,
+    int64_t bt_row_stride, const int32_t* q_lens, const int32_t* k_lens,
+    const int32_t* q_starts, const int32_t* q_pos_offsets, int64_t num_rows,
+    int64_t total_query, int64_t max_q_len, int64_t max_k_len,
+    int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim,
+    int64_t block_size, int64_t num_blocks, float scale, int is_causal,
+    int dtype, int64_t partition_tokens, const int32_t* schedule,
+    int64_t num_decode_units, int64_t num_prefill_units, int64_t num_merge_units,
+    int64_t schedule_workspace_bytes, void* workspace, int64_t workspace_bytes, void* stream) {
+  return paged_attention_impl(q, q_strides, k_cache, k_cache_strides, v_cache, v_cache_strides, out, out_strides,
+                              lse, lse_strides, block_table, bt_row_stride, q_lens, k_lens, q_starts,
+                              q_pos_offsets, num_rows, total_query, max_q_len, max_k_len, num_q_heads,
+                              num_kv_heads, head_dim, block_size, num_blocks, scale, is_causal, dtype,
+                              partition_tokens, schedule, num_decode_units, num_prefill_units, num_merge_units,
+                              schedule_workspace_bytes, workspace, workspace_bytes, true, stream);
+}
+
+// ------------------------------------------------------------ no-alloc --
+// Split-K partials of kvhot_paged_attention_noalloc: a device-global array,
+// one copy on every device the library runs on, held until the process ends.
+// In host code `scratch` names a host-side stand-in, not device memory: its
+// device address comes from hipGetSymbolAddress, once per device.
+static __device__ __align__(256) unsigned char scratch[KVHOT_NOALLOC_SCRATCH_BYTES];
+
+static std::mutex g_scratch_mutex;
+static void* g_scratch_addr[kMaxDevices];
+
+// Device address of the current device's `scratch`, looked up on the
+// device's first call.  0, or a positive hipError_t.
+static int scratch_address(void** out) {
+  int dev = -1;
+  const hipError_t de = hipGetDevice(&dev);
+  if (de != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    (void)hipGetLastError();
+    return set_error(de != hipSuccess ? static_cast<int>(de) : static_cast<int>(hipErrorInvalidDevice),
+                     "paged_attention_noalloc: no usable current device");
+  }
+  std::lock_guard<std::mutex> guard(g_scratch_mutex);
+  if (!g_scratch_addr[dev]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+      (void)hipGetLastError();
+      return set_error(e != hipSuccess ? static_cast<int>(e) : static_cast<int>(hipErrorInvalidSymbol),
+                       std::string("paged_attention_noalloc: hipGetSymbolAddress(scratch): ") +
+                           hipGetErrorString(e));
+    }
+    g_scratch_addr[dev] = p;
+  }
+  *out = g_scratch_addr[dev];
+  return 0;
+}
+
+extern "C" int kvhot_paged_attention_noalloc(
+    const void* q, const int64_t q_strides[3], const void* k_cache,
+    const int64_t k_cache_strides[4], const void* v_cache,
+    const int64_t v_cache_strides[4], void* out, const int64_t out_strides[3],
+    float* lse, const int64_t lse_strides[2], const int32_t* block_table,
+    int64_t bt_row_stride, const int32_t* q_lens, const int32_t* k_lens,
+    const int32_t* q_starts, const int32_t* q_pos_offsets, int64_t num_rows,
+    int64_t total_query, int64_t max_q_len, int64_t max_k_len,
+    int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim,
+    int64_t block_size, int64_t num_blocks, float scale, int is_causal,
+    int dtype, int64_t partition_tokens, const int32_t* schedule,
+    int64_t num_decode_units, int64_t num_prefill_units, int64_t num_merge_units,
+    int64_t schedule_workspace_bytes, void* stream) {
+  clear_error();
+  int64_t need = 0;
+  if (schedule) {
+    need = num_merge_units > 0 ? schedule_workspace_bytes : 0;
+  } else {
+    need = kvhot_paged_attention_workspace_bytes(num_rows, total_query, max_q_len, max_k_len, num_q_heads,
+                                                 num_kv_heads, head_dim, block_size, partition_tokens, dtype);
+    if (need < 0) return set_error(static_cast<int>(need), "paged_attention_noalloc: bad sizes");
+  }
+  if (need > KVHOT_NOALLOC_SCRATCH_BYTES)
+    return set_error(KVHOT_EWORKSPACE, "paged_attention_noalloc: the call needs " + std::to_string(need) +
+                                           " bytes of split-K partials, more than its scratch of " +
+                                           std::to_string(static_cast<int64_t>(KVHOT_NOALLOC_SCRATCH_BYTES)));
+  void* ws = nullptr;
+  if (need > 0) {
+    const int rc = scratch_address(&ws);
+    if (rc != 0) return rc;
+  }
+  return paged_attention_impl(q, q_strides, k_cache, k_cache_strides, v_cache, v_cache_strides, out, out_strides,
+                              lse, lse_strides, block_table, bt_row_stride, q_lens, k_lens, q_starts,
+                              q_pos_offsets, num_rows, total_query, max_q_len, max_k_len, num_q_heads,
+                              num_kv_heads, head_dim, block_size, num_blocks, scale, is_causal, dtype,
+                              partition_tokens, schedule, num_decode_units, num_prefill_units, num_merge_units,
+                              schedule_workspace_bytes, ws, need > 0 ? int64_t{KVHOT_NOALLOC_SCRATCH_BYTES} : 0,
+                              false, stream);
 }

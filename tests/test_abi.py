@@ -25,7 +25,7 @@ def lib():
 
 def test_library_exports_every_declared_symbol(lib):
     names = declared_functions()
-    assert len(names) == 8
+    assert len(names) == 9
     for n in names:
         assert hasattr(lib, n), n
     assert sorted(sea_module("_lib").SIGNATURES) == names
@@ -114,6 +114,29 @@ def test_attention_checks_the_schedule_workspace(lib):
     assert lib.kvhot_paged_attention(*bad) == -1
     bad[33] = -1
     assert lib.kvhot_paged_attention(*bad) == -1
+
+
+@no_gpu
+def test_noalloc_rejects_calls_beyond_its_scratch(lib):
+    """The no-alloc variant holds at most 32 MiB of split-K partials; a call
+    that needs more is KVHOT_EWORKSPACE before it touches a device."""
+    assert sea_module("_lib").NOALLOC_SCRATCH_BYTES == 32 << 20
+    q3, c4, l2 = _i64(4096, 128, 1), _i64(16384, 1024, 128, 1), _i64(32, 1)
+    f = FAKE
+    # no schedule: 64 rows of up to 65536 keys in 32-key partitions -> 64 x 8 x 2048 partials of 2064 bytes
+    args = [f, q3, f, c4, f, c4, f, q3, f, l2, f, 4096, f, f, f, f,
+            64, 64, 1, 65536, 32, 8, 128, 16, 1 << 20, 0.1, 1, 2, 32, None, 0, 0, 0, 0, None]
+    assert lib.kvhot_paged_attention_noalloc(*args) == -3
+    msg = lib.kvhot_last_error()
+    assert str(64 * 8 * 2048 * 4 * 129 * 4).encode() in msg and b"33554432" in msg
+    # a schedule whose merge units need one byte more than the scratch
+    sched = list(args)
+    sched[29:34] = [f, 16, 0, 1, (32 << 20) + 1]
+    assert lib.kvhot_paged_attention_noalloc(*sched) == -3
+    # invalid sizes are reported as such
+    bad = list(args)
+    bad[20] = 30
+    assert lib.kvhot_paged_attention_noalloc(*bad) == -1
 
 
 def test_workspace_bytes(lib):
