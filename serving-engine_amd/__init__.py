@@ -19,10 +19,13 @@ from .model_runner import (
     PAGED_HIP_ATTN_IMPL,
     _PagedKVCache,
     allocate_kv_cache,
+    forward_step,
     hip_paged_attention_forward,
     num_blocks_for_memory,
     register_attention,
+    sample_step,
     step_inputs,
+    step_token_ids,
 )
 from .decode_graph import DecodeStepGraph
 from .request import Request, RequestPhase, RequestStatus, SchedulerOutput
@@ -45,9 +48,12 @@ __all__ = [
     "allocate_kv_cache",
     "build_paged_batch_metadata",
     "build_slot_mapping",
+    "forward_step",
     "hip_paged_attention_forward",
     "num_blocks_for_memory",
     "paged_flash_attention",
     "register_attention",
+    "sample_step",
     "step_inputs",
+    "step_token_ids",
 ]

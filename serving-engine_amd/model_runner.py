@@ -13,8 +13,13 @@ serving_engine/model_runner.py, running on libkvhot.
 * ``allocate_kv_cache`` / ``num_blocks_for_memory``: the pool of
   serving_engine/model_runner.py:101-125.
 * ``step_inputs``: a step's metadata, after its copy-on-write block copies.
+* ``forward_step`` / ``sample_step``: ModelRunner.forward and engine.step's
+  greedy sampling (serving_engine/model_runner.py:131-212,
+  serving_engine/engine.py:92-116) with the logits computed for each row's
+  last token only (``logits_to_keep``), the argmax taken on the device and
+  one batched host copy of the step's tokens.
 
-Model loading, tokenisation and sampling stay with the caller.
+Model loading and tokenisation stay with the caller.
 """
 from __future__ import annotations
 
@@ -23,6 +28,7 @@ import torch
 from . import _lib
 from .block import BLOCK_SIZE
 from .paged_attention_kernel import build_paged_batch_metadata, paged_flash_attention
+from .request import RequestPhase
 
 PAGED_HIP_ATTN_IMPL = "paged|hip"
 
@@ -204,3 +210,53 @@ def step_inputs(scheduler_output, device="cuda", cache=None):
         cache.copy_blocks(list(src), list(dst))
     meta = build_paged_batch_metadata(scheduler_output, device=device)
     return meta, meta.get("slot_mapping"), meta.get("positions")
+
+
+def step_token_ids(scheduler_output):
+    """The step's input tokens, rows in scheduled order
+    (serving_engine/model_runner.py:150-163): a prefill row's chunk of its
+    tokens from num_computed_tokens on, a decode row's last output token."""
+    toks = []
+    for req in scheduler_output.scheduled_requests:
+        if req.phase == RequestPhase.NEEDS_PREFILL:
+            c0 = req.num_computed_tokens
+            toks += req.all_token_ids()[c0:c0 + scheduler_output.prefill_chunk_sizes[req.request_id]]
+        else:
+            toks.append(req.output_token_ids[-1])
+    return toks
+
+
+def forward_step(model, scheduler_output, cache, device="cuda"):
+    """ModelRunner.forward (serving_engine/model_runner.py:131-212) on the
+    paged|hip path: the step's copy-on-write copies, metadata, one forward
+    over the flattened batch, and the last token's logits of each scheduled
+    row, [rows, vocab].  The reference computes logits for every token and
+    then keeps one per row (:209-212); here ``logits_to_keep`` names those
+    rows' last positions, so the LM head runs on one row per request.  Every
+    scheduled row must have at least one query token (the scheduler only
+    schedules such rows)."""
+    meta, slots, pos = step_inputs(scheduler_output, device, cache)
+    ids = torch.tensor([step_token_ids(scheduler_output)], dtype=torch.int64).to(device, non_blocking=True)
+    keep = (meta["q_starts"] + meta["q_lens"] - 1).long()
+    with torch.no_grad():
+        out = model(input_ids=ids, position_ids=pos.view(1, -1), cache=cache, write_index=slots,
+                    paged_metadata=meta, use_cache=False, logits_to_keep=keep)
+    return out.logits[0]
+
+
+def sample_step(model, scheduler, cache, device="cuda"):
+    """One greedy engine iteration (serving_engine/engine.py:92-116):
+    schedule, forward_step, argmax on the device, then a single host copy of
+    the step's tokens (the reference reads them back one ``.item()`` per
+    request), appended to the requests that produced a real next token.
+    Returns (scheduler output, the step's last-token logits)."""
+    out = scheduler.schedule()
+    if not out.scheduled_requests:
+        return out, None
+    logits = forward_step(model, out, cache, device)
+    tokens = logits.argmax(-1).cpu().tolist()
+    for req, tok in zip(out.scheduled_requests, tokens):
+        if req.phase == RequestPhase.NEEDS_DECODE or req.request_id in out.prefill_final_chunk:
+            req.output_token_ids.append(int(tok))
+    scheduler.update_after_step(out)
+    return out, logits
