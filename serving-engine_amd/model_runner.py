@@ -97,22 +97,27 @@ class _PagedKVCache:
         each (serving_engine/model_runner.py:42-45)."""
         return self.kv_cache[layer_idx, 0], self.kv_cache[layer_idx, 1]
 
-    def copy_blocks(self, src_block_ids, dst_block_ids):
+    def copy_blocks(self, src_block_ids, dst_block_ids, validate=True):
         """Copy-on-write data mover: kv_cache[:, :, dst[i]] = kv_cache[:, :, src[i]]
-        for every layer, K and V, in one launch.  Destinations must be unique
-        and disjoint from the sources (checked when the ids are host data)."""
+        for every layer, K and V, in one launch.  Ids must lie in the pool,
+        destinations must be unique and disjoint from the sources (pairs that
+        overlap would race).  Checked on the host before the copy: host ids
+        as they are, device ids after one copy to the host (a synchronisation;
+        ``validate=False`` skips it for ids the caller has already checked --
+        the kernel then skips ids outside the pool)."""
         src = torch.as_tensor(src_block_ids, dtype=torch.int64)
         dst = torch.as_tensor(dst_block_ids, dtype=torch.int64)
         if src.shape != dst.shape or src.dim() != 1:
             raise ValueError("src_block_ids and dst_block_ids must be 1-D of equal length")
         n = self.kv_cache.shape[2]
-        if src.device.type == "cpu" and dst.device.type == "cpu" and src.numel():
-            if int(src.min()) < 0 or int(src.max()) >= n or int(dst.min()) < 0 or int(dst.max()) >= n:
+        if validate and src.numel():
+            hs, hd = src.cpu(), dst.cpu()  # host ids as they are; device ids: one synchronising copy
+            if int(hs.min()) < 0 or int(hs.max()) >= n or int(hd.min()) < 0 or int(hd.max()) >= n:
                 raise IndexError(f"block id out of range [0, {n})")
-            d = set(dst.tolist())
-            if len(d) != dst.numel():
+            d = set(hd.tolist())
+            if len(d) != hd.numel():
                 raise ValueError("destination block ids must be unique")
-            if d & set(src.tolist()):
+            if d & set(hs.tolist()):
                 raise ValueError("a destination block is also a source block")
         if src.numel() == 0:
             return
@@ -201,14 +206,18 @@ def step_inputs(scheduler_output, device="cuda", cache=None):
     ``slot_mapping`` is the write_index and ``positions`` the position ids.
     With ``cache``, the step's copy-on-write pairs
     (scheduler_output.blocks_to_copy, from scheduler.Scheduler) are copied
-    first, on the same stream, so the step's appends land in the copies."""
+    first, on the same stream, so the step's appends land in the copies, and
+    the step's block tables are checked against the pool (IndexError for a
+    block outside it, as the reference's index_copy_ raises on an out-of-pool
+    write slot)."""
     copies = getattr(scheduler_output, "blocks_to_copy", None)
     if copies:
         if cache is None:
             raise ValueError("the step has copy-on-write block copies: pass the cache")
         src, dst = zip(*copies)
         cache.copy_blocks(list(src), list(dst))
-    meta = build_paged_batch_metadata(scheduler_output, device=device)
+    meta = build_paged_batch_metadata(scheduler_output, device=device,
+                                      num_blocks=cache.kv_cache.shape[2] if cache is not None else None)
     return meta, meta.get("slot_mapping"), meta.get("positions")
 
 

@@ -198,12 +198,18 @@ def paged_flash_attention(q, k_cache, v_cache, metadata, num_q_heads, num_kv_hea
     return o, l
 
 
-def build_paged_batch_metadata(scheduler_output, device="cuda"):
+def build_paged_batch_metadata(scheduler_output, device="cuda", num_blocks=None):
     """Per-step metadata shared by all layers (serving_engine/paged_attention_kernel.py:163-200).
 
     Prefill rows: n_q = chunk, n_k = num_computed + chunk, q_pos_offset =
     num_computed; decode rows: n_q = 1, n_k = total_len, q_pos_offset =
     total_len - 1.  Block tables are padded with 0 to the longest row.
+    ``num_blocks`` (extension): the pool's block count; the host block tables
+    are then checked before anything is copied: a row whose table covers
+    fewer than n_k tokens, or names a block outside [0, num_blocks), raises
+    IndexError (where the reference's write, index_copy_ at
+    serving_engine/model_runner.py:31-32, raises on an out-of-pool slot; the
+    append kernel itself skips such slots).
     """
     reqs = scheduler_output.scheduled_requests
     r = len(reqs)
@@ -233,6 +239,18 @@ def build_paged_batch_metadata(scheduler_output, device="cuda"):
     for i, t in enumerate(tables):
         if len(t):
             bt_host[i, : len(t)] = t
+    if num_blocks is not None and r:
+        need = (per_row[1] + BLOCK_SIZE - 1) // BLOCK_SIZE
+        have = np.array([len(t) for t in tables], dtype=np.int64)
+        short = np.nonzero(have < need)[0]
+        if short.size:
+            i = int(short[0])
+            raise IndexError(f"row {i}: block table covers {int(have[i]) * BLOCK_SIZE} tokens, "
+                             f"the step reads {int(per_row[1, i])}")
+        used = bt_host[np.arange(max_blocks)[None, :] < need[:, None]]
+        if used.size and (int(used.min()) < 0 or int(used.max()) >= num_blocks):
+            bad = int(used.min()) if int(used.min()) < 0 else int(used.max())
+            raise IndexError(f"block id {bad} outside the pool [0, {num_blocks})")
     dev = torch.device(device)
     if dev.type == "cuda":
         staged = torch.empty(host.shape[0], dtype=torch.int32, pin_memory=True)

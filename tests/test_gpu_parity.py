@@ -130,6 +130,31 @@ def test_append_int32_slots_padding_and_strides(cuda, sea, dtype):
     assert np.array_equal(bits(kv[1, 1]), ev)
 
 
+@pytest.mark.parametrize("head_major", [False, True])
+def test_update_writes_then_gathers(cuda, sea, head_major):
+    """_PagedKVCache.update, the eager path's write then dense gather
+    (reference serving_engine/model_runner.py:34-40), on both pool layouts:
+    the layer's K/V bit-exactly as the oracle's append leaves them, and the
+    gathered rows bit-exactly those slots of the flat [N * 16, Hkv, D] view."""
+    announce(f"_PagedKVCache.update, head_major={head_major}")
+    g = torch.Generator(device=cuda).manual_seed(17)
+    kv = sea.allocate_kv_cache(2, 12, 4, 64, dtype=torch.bfloat16, device=cuda, head_major=head_major)
+    kv.view(torch.int16).random_(generator=g)
+    key = torch.randn(1, 4, 7, 64, generator=g, device=cuda).to(torch.bfloat16)
+    val = torch.randn(1, 4, 7, 64, generator=g, device=cuda).to(torch.bfloat16)
+    write = torch.tensor([3, 17, 18, -1, 100, 191, 0], dtype=torch.int64, device=cuda)
+    read = torch.tensor([17, 3, 5, 191, 18, 120, 0, 17], dtype=torch.int64, device=cuda)
+    kb, vb = bits(kv[1, 0]), bits(kv[1, 1])
+    k_read, v_read = sea._PagedKVCache(kv).update(key, val, 1, read, write)
+    torch.cuda.synchronize()
+    ek, ev = paged_ref.reshape_and_cache(kb, vb, bits(key[0].transpose(0, 1)), bits(val[0].transpose(0, 1)),
+                                         write.cpu().numpy())
+    assert np.array_equal(bits(kv[1, 0]), ek) and np.array_equal(bits(kv[1, 1]), ev)
+    idx = read.cpu().numpy()
+    assert np.array_equal(bits(k_read), ek.reshape(-1, 4, 64)[idx])
+    assert np.array_equal(bits(v_read), ev.reshape(-1, 4, 64)[idx])
+
+
 # ------------------------------------------------------------- block copy --
 
 def test_copy_blocks_bit_exact(cuda, sea, wl):
@@ -143,10 +168,23 @@ def test_copy_blocks_bit_exact(cuda, sea, wl):
     assert np.array_equal(bits(kv), paged_ref.copy_blocks(before, w.copy_src, w.copy_dst))
 
 
-def test_copy_blocks_rejects_overlap(sea):
-    kv = torch.zeros(1, 2, 8, 16, 1, 8)
+def test_copy_blocks_checks_device_ids(cuda, sea):
+    """Ids that live on the device are checked too (one host copy) before
+    the copy: overlapping or duplicate pairs would race on the device."""
+    announce("copy_blocks with device ids")
+    kv = torch.zeros(1, 2, 8, 16, 1, 8, device=cuda)
+    cache = sea._PagedKVCache(kv)
+    ids = lambda x: torch.tensor(x, device=cuda)
     with pytest.raises(ValueError):
-        sea._PagedKVCache(kv).copy_blocks([1, 2], [2, 3])
+        cache.copy_blocks(ids([1, 2]), ids([2, 3]))
+    with pytest.raises(ValueError):
+        cache.copy_blocks(ids([1, 2]), ids([4, 4]))
+    with pytest.raises(IndexError):
+        cache.copy_blocks(ids([1]), ids([8]))
+    kv[0, 0, 1] = 1.0
+    cache.copy_blocks(ids([1]), ids([5]))
+    torch.cuda.synchronize()
+    assert torch.equal(kv[0, 0, 5], kv[0, 0, 1]) and float(kv[0, 0, 5].min()) == 1.0
 
 
 # ---------------------------------------------------------- slot mapping --
