@@ -35,7 +35,12 @@ on a copy of the pool stored block-wise as [Hkv, 16, D]
 (allocate_kv_cache(head_major=True); same shape, values and results; not the
 headline, which keeps the reference's layout).  cpu_baseline = the reference's eager
 PyTorch path (restated in oracle/eager.py) on this host's cores, on one layer
-of the same batch.
+of the same batch.  copy = kvhot_copy_blocks over the prefix-sharing
+workload's 256 copy-on-write pairs on a 32-layer pool (1 GiB read and written
+per launch), GB/s against 8 TB/s.  prefill.decode_rows = the mixed
+workload's 56 decode rows alone, GB/s.  host_step = host time per engine step
+of the metadata and of the attention launch list.  Every per-launch figure is
+a median over --kernel-reps HIP-event timings.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload 2]
        python bench.py --copy-probe   # kvhot_copy_blocks of 256 MiB each way
@@ -71,12 +76,14 @@ def parse():
                     help="pool stored block-wise as [Hkv, block_size, D] (allocate_kv_cache(head_major=True))")
     ap.add_argument("--layers", type=int, default=32)
     ap.add_argument("--partition-tokens", type=int, default=0)
-    ap.add_argument("--kernel-reps", type=int, default=10, help="passes over all layers for the kernel timing")
+    ap.add_argument("--kernel-reps", type=int, default=20,
+                    help="timed passes over all layers for the per-launch figures (their median is reported)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-prefill", action="store_true", help="skip the prefill MFMA measurement")
     ap.add_argument("--prefill-only", action="store_true",
                     help="only the prefill measurement (for counter runs); prints its JSON object")
     ap.add_argument("--no-engine", action="store_true", help="skip the engine tokens/s measurement")
+    ap.add_argument("--no-copy", action="store_true", help="skip the copy-on-write block copy measurement")
     ap.add_argument("--engine-only", action="store_true", help="only the engine measurement")
     ap.add_argument("--engine-steps", type=int, default=16)
     ap.add_argument("--engine-cpu-layers", type=int, default=2)
@@ -84,6 +91,45 @@ def parse():
     ap.add_argument("--copy-probe", action="store_true",
                     help="only run kvhot_copy_blocks over 256 MiB each way, 5 times (counter calibration)")
     return ap.parse_args()
+
+
+def median_pass_us(body, reps):
+    """Median device time of `reps` runs of body(), each bracketed by HIP
+    events on the current stream, in microseconds."""
+    import torch
+
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+    torch.cuda.synchronize()
+    for a, b in ev:
+        a.record()
+        body()
+        b.record()
+    torch.cuda.synchronize()
+    return statistics.median(a.elapsed_time(b) * 1e3 for a, b in ev)
+
+
+def host_threads():
+    """Host threads for the CPU baselines: every CPU this process may run on,
+    within OMP_NUM_THREADS when that is set (a shared host's share)."""
+    n = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    omp = os.environ.get("OMP_NUM_THREADS", "")
+    if omp.isdigit() and int(omp) > 0:
+        n = min(n, int(omp))
+    return max(1, n)
+
+
+def cpu_model():
+    """The host CPU's model string (/proc/cpuinfo), or the platform's."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+
+    return platform.processor() or platform.machine()
 
 
 def recorded_traffic(workload: int):
@@ -142,7 +188,7 @@ def main():
         sea = importlib.import_module("serving-engine_amd")
         wl = importlib.import_module("serving-engine_amd.workloads")
         print(json.dumps({"prefill": prefill_measure(sea, wl, torch.device("cuda:0"),
-                                                     reps=max(1, args.kernel_reps // 2))}), flush=True)
+                                                     reps=max(1, args.kernel_reps))}), flush=True)
         return
 
     import torch
@@ -196,13 +242,10 @@ def main():
     reps = max(1, args.kernel_reps)
 
     def per_launch_us(body):
+        """Median over `reps` passes of (pass time / layers), eager and as
+        replays of one recorded graph of the pass."""
         torch.cuda.synchronize()
-        start.record()
-        for _ in range(reps):
-            body()
-        end.record()
-        torch.cuda.synchronize()
-        eager = start.elapsed_time(end) * 1e3 / (reps * layers)
+        eager = median_pass_us(lambda: body(), reps) / layers
         graph = torch.cuda.CUDAGraph()
         side = torch.cuda.Stream(dev)
         side.wait_stream(torch.cuda.current_stream(dev))
@@ -214,12 +257,7 @@ def main():
             body()
         graph.replay()
         torch.cuda.synchronize()
-        start.record()
-        for _ in range(reps):
-            graph.replay()
-        end.record()
-        torch.cuda.synchronize()
-        return start.elapsed_time(end) * 1e3 / (reps * layers), eager
+        return median_pass_us(graph.replay, reps) / layers, eager
 
     attn_us, attn_eager_us = per_launch_us(lambda: [attention(i) for i in range(layers)])
     attn_gbs = attn_bytes / (attn_us * 1e-6) / 1e9
@@ -243,18 +281,22 @@ def main():
                       "avg_launch_us": round(hm_us, 3), "achieved": round(hm_gbs, 2), "unit": "GB/s",
                       "frac": round(hm_gbs / HBM_PEAK_GBS, 4)}
 
+    host_cost = host_step_cost(sea, w, dev, pt)
+
     prefill = None
     if not args.no_prefill:
-        prefill = prefill_measure(sea, wl, dev, reps=max(1, args.kernel_reps // 2))
+        prefill = prefill_measure(sea, wl, dev, reps=max(1, args.kernel_reps))
 
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(w, t, layer=0, budget_s=args.cpu_seconds, attn_bytes=attn_bytes + append_bytes)
 
+    del t, cache, blocks
+    torch.cuda.empty_cache()
+    copy = None if args.no_copy else copy_measure(sea, wl, dev, reps=reps)
+
     engine = None
     if not args.no_engine:
-        del t, cache, blocks
-        torch.cuda.empty_cache()
         engine = engine_measure(dev, steps=args.engine_steps,
                                 cpu_layers=0 if args.no_cpu_baseline else args.engine_cpu_layers)
 
@@ -302,8 +344,11 @@ def main():
         "append": {"avg_launch_us": round(append_us, 3), "eager_call_us": round(append_eager_us, 3),
                    "algorithmic_bytes": append_bytes,
                    "gbs": round(append_bytes / (append_us * 1e-6) / 1e9, 2)},
+        "host_step": host_cost,
         "cpu_baseline": cpu,
     }
+    if copy is not None:
+        line["copy"] = copy
     if prefill is not None:
         line["prefill"] = prefill
     if engine is not None:
@@ -466,6 +511,7 @@ def engine_measure(dev, steps=16, warmup=2, cpu_layers=2):
         "step": "recorded once in a HIP graph (DecodeStepGraph) and replayed: per step the host builds the "
                 "metadata and the attention launch list, two pinned copies, one graph launch",
         "ms_per_step": round(ms, 3),
+        "ms_per_step_per_layer": round(ms / layers, 4),
         "tokens_per_s": round(len(lens) / (ms * 1e-3), 1),
         "wall_tokens_per_s": round(len(lens) * steps / gwall, 1),
         "graph_recordings": graph.recordings,
@@ -479,16 +525,22 @@ def engine_measure(dev, steps=16, warmup=2, cpu_layers=2):
     return res
 
 
-def engine_cpu_baseline(num_layers, ctx, tables, n, steps=2):
-    """The same decode step on the host CPU with `num_layers` layers and the
-    reference's eager paged attention (restated in oracle/eager.py, per-row
-    form) as the attention function: output tokens/s of that model."""
+def engine_cpu_baseline(num_layers, ctx, tables, n, steps=3):
+    """The same decode step on the host CPU with the reference's eager paged
+    attention (restated in oracle/eager.py, per-row form) as the attention
+    function: output tokens/s of that model with 1 and with `num_layers`
+    layers (median step time of `steps` steps after one warm-up each), and
+    from those two the tokens/s of the 32-layer model the GPU runs (a step is
+    a fixed part -- embedding, final norm, LM head, argmax -- plus one
+    per-layer part per layer, so t(32) = t(1) + 31 * (t(L) - t(1)) / (L - 1))."""
     import torch
     from transformers import AttentionInterface
 
     from oracle import eager
 
     sea = importlib.import_module("serving-engine_amd")
+    threads = host_threads()
+    torch.set_num_threads(threads)
 
     def cpu_attention(module, query, key, value, attention_mask, scaling, **kw):
         kc, vc = kw["cache"].blocks(module.layer_idx)
@@ -498,40 +550,57 @@ def engine_cpu_baseline(num_layers, ctx, tables, n, steps=2):
         return o.unsqueeze(0), None
 
     AttentionInterface.register("paged|eager_cpu", cpu_attention)
-    cfg = _llama_8b_config(num_layers)
-    model = _random_llama(cfg, torch.device("cpu"), "paged|eager_cpu")
-    kv = torch.randn(num_layers, 2, n, 16, 8, 128, dtype=torch.float32).div_(math.sqrt(128)).to(torch.bfloat16)
-    cache = sea._PagedKVCache.__new__(sea._PagedKVCache)  # CPU pool: only .blocks() is used here
-    cache.kv_cache, cache.num_kv_heads, cache.head_dim = kv, 8, 128
-    lens = list(ctx)
-    tok = torch.zeros(len(lens), dtype=torch.int64)
 
-    def step():
-        nonlocal tok
-        rows = [(1, ln + 1, ln, tb) for ln, tb in zip(lens, tables)]
-        slots = torch.tensor([tb[ln // 16] * 16 + ln % 16 for ln, tb in zip(lens, tables)], dtype=torch.int64)
-        pos = torch.tensor(lens, dtype=torch.int64).view(1, -1)
-        with torch.no_grad():
-            out = model(input_ids=tok.view(1, -1), position_ids=pos, cache=cache, write_index=slots, rows=rows,
-                        use_cache=False)
-        tok = out.logits[0].argmax(-1)
-        for i in range(len(lens)):
-            lens[i] += 1
+    def step_seconds(layers):
+        cfg = _llama_8b_config(layers)
+        model = _random_llama(cfg, torch.device("cpu"), "paged|eager_cpu")
+        kv = torch.randn(layers, 2, n, 16, 8, 128, dtype=torch.float32).div_(math.sqrt(128)).to(torch.bfloat16)
+        cache = sea._PagedKVCache.__new__(sea._PagedKVCache)  # CPU pool: only .blocks() is used here
+        cache.kv_cache, cache.num_kv_heads, cache.head_dim = kv, 8, 128
+        lens = list(ctx)
+        tok = torch.zeros(len(lens), dtype=torch.int64)
 
-    step()  # warm-up
-    t0 = time.perf_counter()
-    for _ in range(steps):
-        step()
-    sec = (time.perf_counter() - t0) / steps
+        def step():
+            nonlocal tok
+            rows = [(1, ln + 1, ln, tb) for ln, tb in zip(lens, tables)]
+            slots = torch.tensor([tb[ln // 16] * 16 + ln % 16 for ln, tb in zip(lens, tables)], dtype=torch.int64)
+            pos = torch.tensor(lens, dtype=torch.int64).view(1, -1)
+            with torch.no_grad():
+                out = model(input_ids=tok.view(1, -1), position_ids=pos, cache=cache, write_index=slots, rows=rows,
+                            use_cache=False)
+            tok = out.logits[0].argmax(-1)
+            for i in range(len(lens)):
+                lens[i] += 1
+
+        step()  # warm-up
+        times = []
+        for _ in range(steps):
+            t0 = time.perf_counter()
+            step()
+            times.append(time.perf_counter() - t0)
+        return statistics.median(times)
+
+    t1 = step_seconds(1)
+    tl = step_seconds(num_layers) if num_layers > 1 else t1
+    per_layer = (tl - t1) / (num_layers - 1) if num_layers > 1 else t1
+    t32 = t1 + 31 * per_layer
+    batch = len(ctx)
     return {
-        "tokens_per_s": round(len(lens) / sec, 2),
+        "tokens_per_s": round(batch / tl, 2),
+        "tokens_per_s_at_32_layers": round(batch / t32, 2),
         "unit": "tokens/s",
-        "cores": torch.get_num_threads(),
+        "cores": threads,
+        "cpu_model": cpu_model(),
+        "host_cpus": os.cpu_count(),
         "kind": "port",
-        "sample": f"{num_layers}-layer model of the same shape on the host CPU (bf16, torch), batch {len(lens)}, "
-                  f"eager paged attention (per-row form), mean of {steps} steps after 1 warm-up; "
-                  f"{sec * 1e3:.0f} ms per step",
+        "sample": f"1- and {num_layers}-layer models of the same shape on the host CPU (bf16, torch, {threads} "
+                  f"threads), batch {batch}, eager paged attention (per-row form), median of {steps} steps after "
+                  f"1 warm-up each: {t1 * 1e3:.0f} and {tl * 1e3:.0f} ms per step; 32 layers extrapolated "
+                  f"as t(1) + 31 x the per-layer time",
         "layers": num_layers,
+        "ms_per_step": {"1_layer": round(t1 * 1e3, 2), f"{num_layers}_layers": round(tl * 1e3, 2),
+                        "32_layers_extrapolated": round(t32 * 1e3, 2)},
+        "ms_per_layer": round(per_layer * 1e3, 2),
     }
 
 
@@ -545,8 +614,9 @@ def prefill_measure(sea, wl, dev, reps, layers=16):
 
     full = wl.make_workload(3)
     rows = dataclasses.replace(full, rows=[r for r in full.rows if r.prefill])
+    decode = dataclasses.replace(full, rows=[r for r in full.rows if not r.prefill])
     out = {}
-    for key, w in (("prefill_rows", rows), ("mixed_batch", full)):
+    for key, w in (("prefill_rows", rows), ("decode_rows", decode), ("mixed_batch", full)):
         t = wl.make_tensors(w, dev, num_layers=layers)
         cache = sea._PagedKVCache(t.kv_cache)
         meta = sea.build_paged_batch_metadata(w.scheduler_output(), device=dev)
@@ -560,13 +630,7 @@ def prefill_measure(sea, wl, dev, reps, layers=16):
 
         run()
         torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        for _ in range(reps):
-            run()
-        e1.record()
-        torch.cuda.synchronize()
-        out[key] = e0.elapsed_time(e1) * 1e3 / (reps * layers)
+        out[key] = median_pass_us(run, reps) / layers
         del t, cache, blocks
         torch.cuda.empty_cache()
     flops = rows.prefill_flops()
@@ -582,7 +646,89 @@ def prefill_measure(sea, wl, dev, reps, layers=16):
         "unit": "TFLOP/s",
         "frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4),
         "mixed_batch_call_us": round(out["mixed_batch"], 3),
+        "decode_rows": {
+            "rows": len(decode.rows),
+            "avg_call_us": round(out["decode_rows"], 3),
+            "algorithmic_bytes": decode.decode_algorithmic_bytes(),
+            "achieved": round(decode.decode_algorithmic_bytes() / (out["decode_rows"] * 1e-6) / 1e9, 2),
+            "unit": "GB/s",
+            "frac": round(decode.decode_algorithmic_bytes() / (out["decode_rows"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+        },
+        "timing": f"median over {reps} passes of {layers} calls, HIP events",
     }
+
+
+def copy_measure(sea, wl, dev, reps, layers=32, per_rep=4):
+    """kvhot_copy_blocks for the prefix-sharing workload's copy-on-write
+    pairs (its 256 partially filled last blocks) over a `layers`-layer pool:
+    one launch reads and writes every layer's K and V block of each pair.
+    Median over `reps` HIP-event timings of `per_rep` back-to-back launches;
+    GB/s of read + written bytes against 8 TB/s."""
+    import torch
+
+    w = wl.make_workload(4)
+    kv = torch.empty(layers, 2, w.num_blocks, w.block_size, w.num_kv_heads, w.head_dim, dtype=w.dtype,
+                     device=dev)
+    kv.view(torch.int16).random_(generator=torch.Generator(device=dev).manual_seed(4))
+    cache = sea._PagedKVCache(kv)
+    src = torch.as_tensor(w.copy_src, dtype=torch.int64)
+    dst = torch.as_tensor(w.copy_dst, dtype=torch.int64)
+    cache.copy_blocks(src, dst)  # the pairs are checked once, on the host
+    src_d, dst_d = src.to(dev), dst.to(dev)
+
+    def body():
+        for _ in range(per_rep):
+            cache.copy_blocks(src_d, dst_d, validate=False)
+
+    body()
+    us = median_pass_us(body, reps) / per_rep
+    block_bytes = w.block_size * w.num_kv_heads * w.head_dim * kv.element_size()
+    moved = 2 * len(src) * layers * 2 * block_bytes
+    gbs = moved / (us * 1e-6) / 1e9
+    del kv, cache
+    torch.cuda.empty_cache()
+    return {
+        "workload": w.name,
+        "kernel": "kvhot_copy_blocks",
+        "pairs": len(src),
+        "layers": layers,
+        "bytes_per_launch": moved,
+        "median_launch_us": round(us, 3),
+        "roofline_us": round(moved / (HBM_PEAK_GBS * 1e3), 3),
+        "achieved": round(gbs, 2),
+        "peak": HBM_PEAK_GBS,
+        "unit": "GB/s",
+        "frac": round(gbs / HBM_PEAK_GBS, 4),
+        "timing": f"median over {reps} HIP-event timings of {per_rep} back-to-back launches",
+    }
+
+
+def host_step_cost(sea, w, dev, pt, n=30):
+    """Host time per engine step of build_paged_batch_metadata (host arrays,
+    one pinned copy, the slot-mapping launch) and of the attention launch
+    list (kvhot_paged_attention_schedule and its upload), which one step
+    builds once for all its layers: medians of n steps, in microseconds."""
+    import torch
+
+    pak = importlib.import_module("serving-engine_amd.paged_attention_kernel")
+    lib = importlib.import_module("serving-engine_amd._lib")
+    so = w.scheduler_output()
+    dtype = lib.dtype_code(w.dtype)
+    pt = pak.DEFAULT_PARTITION_TOKENS if pt is None else int(pt)
+    tm, tp = [], []
+    for _ in range(n + 1):
+        t0 = time.perf_counter()
+        m = sea.build_paged_batch_metadata(so, device=dev)
+        t1 = time.perf_counter()
+        pak._schedule(m, dev, w.num_q_heads, w.num_kv_heads, w.head_dim, w.block_size, pt, True, dtype)
+        t2 = time.perf_counter()
+        tm.append(t1 - t0)
+        tp.append(t2 - t1)
+    torch.cuda.synchronize()
+    return {"metadata_us": round(statistics.median(tm[1:]) * 1e6, 1),
+            "launch_list_us": round(statistics.median(tp[1:]) * 1e6, 1),
+            "per": "engine step (both serve every layer of the step)",
+            "rows": len(w.rows)}
 
 
 def cpu_baseline(w, t, layer, budget_s, attn_bytes):
@@ -592,7 +738,8 @@ def cpu_baseline(w, t, layer, budget_s, attn_bytes):
 
     from oracle import eager
 
-    threads = torch.get_num_threads()
+    threads = host_threads()
+    torch.set_num_threads(threads)
     q = t.q.cpu()
     nk = t.new_k.transpose(1, 2).squeeze(0).cpu()
     nv = t.new_v.transpose(1, 2).squeeze(0).cpu()
@@ -618,6 +765,8 @@ def cpu_baseline(w, t, layer, budget_s, attn_bytes):
         "value": round(attn_bytes / sec / 1e9, 3),
         "unit": "GB/s",
         "cores": threads,
+        "cpu_model": cpu_model(),
+        "host_cpus": os.cpu_count(),
         "kind": "port",
         "sample": f"one layer of the same batch (append + {'per-row' if per_row else 'whole-batch'} dense "
                   f"masked eager attention, bf16, torch CPU), median of {reps} reps after 1 warm-up; "
