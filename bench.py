@@ -46,6 +46,7 @@ Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload 2]
        python bench.py --copy-probe   # kvhot_copy_blocks of 256 MiB each way
                                       # (counter calibration)
        python bench.py --prefill-only # the prefill measurement alone
+       python bench.py --copy-only    # the copy-on-write block copy measurement alone
 """
 from __future__ import annotations
 
@@ -84,6 +85,8 @@ def parse():
                     help="only the prefill measurement (for counter runs); prints its JSON object")
     ap.add_argument("--no-engine", action="store_true", help="skip the engine tokens/s measurement")
     ap.add_argument("--no-copy", action="store_true", help="skip the copy-on-write block copy measurement")
+    ap.add_argument("--copy-only", action="store_true",
+                    help="only the copy-on-write block copy measurement; prints its JSON object")
     ap.add_argument("--engine-only", action="store_true", help="only the engine measurement")
     ap.add_argument("--engine-steps", type=int, default=16)
     ap.add_argument("--engine-cpu-layers", type=int, default=2)
@@ -179,6 +182,15 @@ def main():
         torch.cuda.set_device(0)
         print(json.dumps({"engine": engine_measure(torch.device("cuda:0"), steps=args.engine_steps,
                                                    cpu_layers=0 if args.no_cpu_baseline else args.engine_cpu_layers)}),
+              flush=True)
+        return
+    if args.copy_only:
+        import torch
+
+        torch.cuda.set_device(0)
+        sea = importlib.import_module("serving-engine_amd")
+        wl = importlib.import_module("serving-engine_amd.workloads")
+        print(json.dumps({"copy": copy_measure(sea, wl, torch.device("cuda:0"), reps=max(1, args.kernel_reps))}),
               flush=True)
         return
     if args.prefill_only:
