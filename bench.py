@@ -96,6 +96,25 @@ def parse():
     return ap.parse_args()
 
 
+def launch_list_desc(meta, w):
+    """The launches of one attention call, from the unit counts of its launch
+    list (kvhot_paged_attention_schedule)."""
+    plans = [p for p in meta.get("_schedules", {}).values() if p is not None]
+    if not plans:
+        return "one attention call on the padded grid (no launch list)"
+    _, n_dec, n_pre, n_mrg, _, n_pfx = plans[0]
+    tt = "BF16" if w.dtype == torch.bfloat16 else "F16"
+    parts = []
+    if n_pfx:
+        parts.append(f"attn_prefill_kernel<{tt},{w.head_dim}> x {n_pfx} shared-prefix units")
+    parts.append(f"attn_decode_kernel<{tt},{w.head_dim}> x {n_dec} waves")
+    if n_mrg:
+        parts.append(f"attn_merge_kernel<{tt},{w.head_dim}> x {n_mrg} units")
+    if n_pre > n_pfx:
+        parts.append(f"attn_prefill_kernel<{tt},{w.head_dim}> x {n_pre - n_pfx} units on a second stream")
+    return "one attention call: " + " + ".join(parts)
+
+
 def median_pass_us(body, reps):
     """Median device time of `reps` runs of body(), each bracketed by HIP
     events on the current stream, in microseconds."""
@@ -340,8 +359,7 @@ def main():
         "pct_of_hbm_peak": round(100.0 * value / HBM_PEAK_GBS, 2),
         "roofline": {
             "bound": "hbm",
-            "kernel": "one attention call: attn_decode_kernel<BF16,128,16> (+ attn_merge_kernel<BF16,128> "
-                      "when the launch plan cuts a row across work-groups; on this workload it cuts none)",
+            "kernel": launch_list_desc(meta, w),
             "achieved": round(attn_gbs, 2),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",

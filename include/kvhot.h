@@ -144,6 +144,13 @@ int64_t kvhot_paged_attention_workspace_bytes(
  * row's metadata and first block, so the wave's first K/V loads depend on
  * nothing else), num_prefill_units per-work-group prefill units (longest
  * first), num_merge_units units, one per decode range cut into parts.
+ * Shared prefixes: when at least 4 decode rows (with causal masking or not)
+ * read the same first 256 or more keys through the same physical blocks, the
+ * keys of that common prefix are attended once, for all of those rows'
+ * queries together, by prefix units on the MFMA prefill path; each row's
+ * decode work-group then reads only its own tail and folds the prefix
+ * partials into its output.  The first *num_prefix_units of the prefill
+ * units are such prefix units (they run before the decode launch).
  * partition_tokens > 0 (a multiple of 32 up to 2^20) first cuts every decode
  * row into partitions of that many keys, which are then never cut further;
  * 0 leaves the cuts to the planner.  *workspace_bytes receives the workspace
@@ -162,7 +169,8 @@ int64_t kvhot_paged_attention_schedule(
     int64_t head_dim, int64_t block_size, int64_t partition_tokens,
     int is_causal, int dtype, int32_t* units, int64_t capacity_units,
     int64_t* num_decode_units, int64_t* num_prefill_units,
-    int64_t* num_merge_units, int64_t* workspace_bytes);
+    int64_t* num_merge_units, int64_t* workspace_bytes,
+    int64_t* num_prefix_units);
 
 /*
  * Paged attention forward over a ragged batch of rows (prefill chunks and
@@ -179,7 +187,7 @@ int64_t kvhot_paged_attention_schedule(
  * n_q >= 2 run the chunked-prefill kernel.  max_q_len / max_k_len must bound
  * q_lens / k_lens (they size the grid; no device->host sync is made).
  * schedule: device copy of the units from kvhot_paged_attention_schedule for
- * exactly these lengths and sizes, with its three unit counts, the workspace
+ * exactly these lengths and sizes, with its four unit counts, the workspace
  * size it reported (schedule_workspace_bytes) and a workspace at least that
  * large (a shorter one fails with KVHOT_EWORKSPACE before any launch); or
  * NULL, and then partition_tokens (keys per
@@ -205,7 +213,8 @@ int kvhot_paged_attention(
     int64_t num_blocks, float scale, int is_causal, int dtype,
     int64_t partition_tokens, const int32_t* schedule,
     int64_t num_decode_units, int64_t num_prefill_units,
-    int64_t num_merge_units, int64_t schedule_workspace_bytes,
+    int64_t num_merge_units, int64_t num_prefix_units,
+    int64_t schedule_workspace_bytes,
     void* workspace, int64_t workspace_bytes,
     void* stream);
 
@@ -243,7 +252,8 @@ int kvhot_paged_attention_noalloc(
     int64_t num_blocks, float scale, int is_causal, int dtype,
     int64_t partition_tokens, const int32_t* schedule,
     int64_t num_decode_units, int64_t num_prefill_units,
-    int64_t num_merge_units, int64_t schedule_workspace_bytes,
+    int64_t num_merge_units, int64_t num_prefix_units,
+    int64_t schedule_workspace_bytes,
     void* stream);
 
 #ifdef __cplusplus

@@ -61,21 +61,21 @@ SIGNATURES = {
     "kvhot_paged_attention_schedule": (
         _i64,
         [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _int, _int, _vp, _i64,
-         _i64p, _i64p, _i64p, _i64p],
+         _i64p, _i64p, _i64p, _i64p, _i64p],
     ),
     "kvhot_paged_attention": (
         _int,
         [_vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p,
          _vp, _i64, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64,
          _i64, _i64, _i64, _i64, ctypes.c_float, _int, _int, _i64, _vp, _i64, _i64, _i64, _i64,
-         _vp, _i64, _vp],
+         _i64, _vp, _i64, _vp],
     ),
     "kvhot_paged_attention_noalloc": (
         _int,
         [_vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p,
          _vp, _i64, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64,
          _i64, _i64, _i64, _i64, ctypes.c_float, _int, _int, _i64, _vp, _i64, _i64, _i64, _i64,
-         _vp],
+         _i64, _vp],
     ),
 }
 

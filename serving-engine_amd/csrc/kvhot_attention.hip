@@ -435,6 +435,19 @@ struct WaveAttn {
           ltot > 0.f ? (m[s] + __log2f(ltot)) * kLn2 : -INFINITY;
   }
 
+  // Normalised O (fp32) and log2-domain LSE of m-row s to split-K partial
+  // `slot`, query head hh of its kv head, in the layout of the decode
+  // partials.
+  __device__ void store_partial_blocks(const AttnArgs& a, int s, int64_t slot, int hh, float ltot) const {
+    const float inv = ltot > 0.f ? 1.f / ltot : 0.f;
+    float* op = a.ws_o + (slot * a.G + hh) * D + 4 * g;
+#pragma unroll
+    for (int e = 0; e < EPL; ++e)
+      *reinterpret_cast<f32x4*>(op + 16 * e) = f32x4{o[s][e][0] * inv, o[s][e][1] * inv, o[s][e][2] * inv,
+                                                     o[s][e][3] * inv};
+    if (g == 0) a.ws_lse[slot * a.G + hh] = ltot > 0.f ? m[s] + __log2f(ltot) : -INFINITY;
+  }
+
   // A tile with no masked key whose scores all stay within kLazyRescale of
   // their references.  Returns false, with the state untouched, otherwise.
   // The QK and PV products are fenced off (sched_barrier) from the
@@ -582,6 +595,11 @@ __host__ __device__ inline int decode_splits(int nslices, int W, int Hkv) {
 // key (row, kv head, part); per wave the claim counter, range end and segment
 // description [8]; the slot-pool counter.
 constexpr int kDecInfo = 8;
+// Bit of a decode descriptor's part field: the segment folds in its row's
+// shared-prefix partials.
+constexpr int kPrefixFold = 0x8000;
+// Prefix partials a fold reads per round trip.
+constexpr int kFoldBatch = 8;
 __host__ __device__ constexpr int64_t decode_lds_words(int64_t W, int64_t S, int64_t G, int64_t D) {
   return S * G * D + S * G + 4 * S + (2 + kDecInfo) * W + 1;
 }
@@ -612,7 +630,10 @@ attn_decode_kernel(const AttnArgs a) {
   int d_first = -1;
   if (a.sched) {
     // (row | parts << 16, kvh | part << 16, s0, s1), (query token, visible
-    // keys, physical block of slice s0 or -1, partial index)
+    // keys, physical block of slice s0 or -1, partial index).  part with bit
+    // 15 set (kPrefixFold): the row's shared prefix left `parts` partials
+    // from index pidx in an earlier launch; this segment, the rest of the
+    // row, folds them in and writes the row's output.
     const int4* u = a.sched + 2 * (static_cast<int64_t>(blockIdx.x) * W + wave);
     const int4 u0 = u[0], u1 = u[1];
     const int x = __builtin_amdgcn_readfirstlane(u0.x);
@@ -659,8 +680,11 @@ attn_decode_kernel(const AttnArgs a) {
   kvh = __builtin_amdgcn_readfirstlane(kvh);
   s0 = __builtin_amdgcn_readfirstlane(s0);
   s1 = __builtin_amdgcn_readfirstlane(s1);
+  const bool fold = (part & kPrefixFold) != 0;
   const bool valid = row >= 0 && kvh >= 0 && kvh < a.Hkv && qs >= 0 && qs < a.total_q && s0 >= 0 &&
-                     nparts >= 1 && part < nparts && (nparts == 1 || (pidx >= 0 && pidx < a.num_partials));
+                     nparts >= 1 &&
+                     (fold ? part == kPrefixFold && pidx >= 0 && pidx + nparts <= a.num_partials
+                           : part < nparts && (nparts == 1 || (pidx >= 0 && pidx < a.num_partials)));
   const int kb = 16 * s0;
   const int ke = min(kend, 16 * s1);
   const int nsl = valid && ke > kb ? (ke - kb + 15) / 16 : 0;
@@ -821,6 +845,7 @@ attn_decode_kernel(const AttnArgs a) {
   for (int it = lane; it < G * (D / 4); it += 64) {
     const int hh = it / (D / 4);
     const int d0 = 4 * (it % (D / 4));
+    // The slots' states, weighted against their maximum.
     float mx = -INFINITY;
     for (uint64_t b = slots; b; b &= b - 1) mx = fmaxf(mx, sl[__builtin_ctzll(b) * G + hh]);
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
@@ -833,10 +858,42 @@ attn_decode_kernel(const AttnArgs a) {
         acc += wt * *reinterpret_cast<const f32x4*>(so + (static_cast<int64_t>(w) * G + hh) * D + d0);
       }
     }
+    if (fold) {
+      // The prefix partials, kFoldBatch at a time with all their loads in
+      // flight together (indices past the last partial re-read it, weight 0),
+      // combined with a running maximum.
+      for (int p0 = 0; p0 < nparts; p0 += kFoldBatch) {
+        float lp[kFoldBatch];
+        f32x4 ov[kFoldBatch];
+#pragma unroll
+        for (int k = 0; k < kFoldBatch; ++k) {
+          const int64_t pi = pidx + min(p0 + k, nparts - 1);
+          lp[k] = a.ws_lse[pi * G + hh];
+          ov[k] = *reinterpret_cast<const f32x4*>(a.ws_o + (pi * G + hh) * D + d0);
+        }
+        float cm = mx;
+#pragma unroll
+        for (int k = 0; k < kFoldBatch; ++k) {
+          if (p0 + k >= nparts) lp[k] = -INFINITY;
+          cm = fmaxf(cm, lp[k]);
+        }
+        if (cm == -INFINITY) continue;
+        const float sc = mx == -INFINITY ? 0.f : fast_exp2(mx - cm);
+        acc *= sc;
+        lsum *= sc;
+#pragma unroll
+        for (int k = 0; k < kFoldBatch; ++k) {
+          const float wt = lp[k] == -INFINITY ? 0.f : fast_exp2(lp[k] - cm);
+          lsum += wt;
+          acc += wt * ov[k];
+        }
+        mx = cm;
+      }
+    }
     const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
     const int h = kvh * G + hh;
     const float lse2 = lsum > 0.f ? mx + __log2f(lsum) : -INFINITY;
-    if (nparts == 1) {
+    if (nparts == 1 || fold) {
       st* dp = static_cast<st*>(a.o) + qs * a.o_st + static_cast<int64_t>(h) * a.o_sh + d0;
       *reinterpret_cast<u32x2*>(dp) =
           u32x2{TT::pack2(acc.x * inv, acc.y * inv), TT::pack2(acc.z * inv, acc.w * inv)};
@@ -1080,12 +1137,33 @@ attn_prefill_kernel(const AttnArgs a) {
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63;
-  int row, kvh, qblk;
+  const int QPW = 16 * NM / a.G;  // queries per wave
+  // A unit is a query block of a prefill row (keys from 0, causal), or a
+  // shared-prefix unit: the queries of consecutive decode rows (tokens
+  // qt0 .. qt0 + nqg - 1, one per row) over keys [k0, kend_g) of the prefix
+  // they share, read through `row`'s block table; every such key is visible
+  // to every such query, and the normalised output of query i goes to the
+  // split-K partial pbase + i * pstride instead of the output.
+  int row, kvh, qblk = 0, k0 = 0, kend_g = 0, nqg = 0, off = 0, pbase = 0, pstride = 0;
+  int64_t qs = 0;
+  int q0g = 0;
+  bool prefix = false;
   if (a.sched) {
     const int4 u = a.sched[2 * static_cast<int64_t>(blockIdx.x)];
+    const int4 u1 = a.sched[2 * static_cast<int64_t>(blockIdx.x) + 1];
     row = u.x;
     kvh = u.y;
-    qblk = u.z;
+    prefix = __builtin_amdgcn_readfirstlane(u1.y) > 0;
+    if (prefix) {
+      k0 = u.z;
+      kend_g = u.w;
+      qs = u1.x;
+      nqg = min(u1.y, QPW * kPreWaves);
+      pbase = u1.z;
+      pstride = u1.w;
+    } else {
+      qblk = u.z;
+    }
   } else {
     row = blockIdx.z;
     kvh = blockIdx.x % a.Hkv;
@@ -1095,21 +1173,35 @@ attn_prefill_kernel(const AttnArgs a) {
   kvh = __builtin_amdgcn_readfirstlane(kvh);
   qblk = __builtin_amdgcn_readfirstlane(qblk);
   if (row < 0 || kvh < 0 || kvh >= a.Hkv || qblk < 0) return;
-  const int qlen = a.q_lens[row];
-  if (qlen < 2) return;
-  const int QPW = 16 * NM / a.G;  // queries per wave
-  const int q0g = qblk * QPW * kPreWaves;
-  if (q0g >= qlen) return;
-  const int nqg = min(QPW * kPreWaves, qlen - q0g);
-  const int off = a.q_offs[row];
-  const int klen = a.k_lens[row];
-  const int kend_g = max(a.causal ? min(klen, off + q0g + nqg) : klen, 0);
-  const int64_t qs = a.q_starts[row];
+  if (prefix) {
+    k0 = __builtin_amdgcn_readfirstlane(k0);
+    kend_g = __builtin_amdgcn_readfirstlane(kend_g);
+    qs = __builtin_amdgcn_readfirstlane(static_cast<int>(qs));
+    nqg = __builtin_amdgcn_readfirstlane(nqg);
+    pbase = __builtin_amdgcn_readfirstlane(pbase);
+    pstride = __builtin_amdgcn_readfirstlane(pstride);
+    if (k0 < 0 || k0 % kPreKeys != 0 || kend_g <= k0 || kend_g > a.k_lens[row] || qs < 0 || pbase < 0 ||
+        pstride <= 0 || static_cast<int64_t>(pbase) + static_cast<int64_t>(nqg - 1) * pstride >= a.num_partials)
+      return;
+    off = 1 << 29;  // past every key: the prefix is wholly visible
+  } else {
+    const int qlen = a.q_lens[row];
+    if (qlen < 2) return;
+    q0g = qblk * QPW * kPreWaves;
+    if (q0g >= qlen) return;
+    nqg = min(QPW * kPreWaves, qlen - q0g);
+    off = a.q_offs[row];
+    const int klen = a.k_lens[row];
+    kend_g = max(a.causal ? min(klen, off + q0g + nqg) : klen, 0);
+    qs = a.q_starts[row];
+  }
+  const bool causal = a.causal && !prefix;
+  const int klen = prefix ? kend_g : a.k_lens[row];
   // This wave's queries and the keys they see.
   const int q0 = q0g + wave * QPW;
   const int nq = max(min(QPW, nqg - wave * QPW), 0);
-  const int kend = nq > 0 ? max(a.causal ? min(klen, off + q0 + nq) : klen, 0) : 0;
-  const int qpos_min = a.causal ? off + q0 : INT_MAX;
+  const int kend = nq > 0 ? max(causal ? min(klen, off + q0 + nq) : klen, 0) : 0;
+  const int qpos_min = causal ? off + q0 : INT_MAX;
 
   WA wa;
   wa.setup(a, lane, kvh, qs, q0, nq, off);
@@ -1161,7 +1253,7 @@ attn_prefill_kernel(const AttnArgs a) {
   const __attribute__((address_space(4))) int32_t* btc =
       (const __attribute__((address_space(4))) int32_t*)btrow;
   auto bt_at = [&](int blk) -> int { return btc[min(blk, max(nb_row - 1, 0))]; };
-  int nblk = (16 * hw) / bs, nbo = (16 * hw) % bs;
+  int nblk = (k0 + 16 * hw) / bs, nbo = (k0 + 16 * hw) % bs;
   int nid = nb_row > 0 ? bt_at(nblk) : 0;
 
   // DMA of tile t (the next in order) into ring slot S.  The descriptor of
@@ -1170,7 +1262,7 @@ attn_prefill_kernel(const AttnArgs a) {
   auto issue = [&](int S, int t) {
     if (!issuer) return;
     const uint32_t b = min(static_cast<uint32_t>(max(nid, 0)), nblocks - 1);
-    const int rows = min(max(kend_g - (kPreKeys * t + 16 * hw), 0), 16);
+    const int rows = min(max(kend_g - (k0 + kPreKeys * t + 16 * hw), 0), 16);
     const char* kb = kbase + (static_cast<uint64_t>(b) * ksb + static_cast<uint32_t>(nbo) * kst);
     const char* vb = vbase + (static_cast<uint64_t>(b) * vsb + static_cast<uint32_t>(nbo) * vst);
     const int nrk = __builtin_amdgcn_readfirstlane(rows * static_cast<int>(kst));
@@ -1199,7 +1291,7 @@ attn_prefill_kernel(const AttnArgs a) {
   // t+3 is issued.  After tile t: wait until tile t+1 has landed (this wave's
   // DMAs of tiles t+2 and t+3 may stay in flight), then one barrier.
   constexpr int PER_TILE = 2 * NI;  // DMA instructions per issuing wave and tile
-  const int ntiles = (kend_g + kPreKeys - 1) / kPreKeys;
+  const int ntiles = (kend_g - k0 + kPreKeys - 1) / kPreKeys;
   auto finish = [&](int t) {
     if (t + 1 < ntiles) {
       const int later = min(t + 3, ntiles - 1) - (t + 1);
@@ -1222,7 +1314,7 @@ attn_prefill_kernel(const AttnArgs a) {
   // per four tiles (a single path for the accumulators); a fast tile that
   // would have to move a reference -- always the first -- and every other
   // tile take the general path one at a time.
-  const int nfull = (a.causal ? min(kend, qpos_min + 1) : kend) / kPreKeys;
+  const int nfull = ((causal ? min(kend, qpos_min + 1) : kend) - k0) / kPreKeys;
   auto fast = [&](int S, int t) -> bool {
     if (t + 3 < ntiles) issue((S + 3) % kPreSlots, t + 3);
     const char* kt = slot(S);
@@ -1231,7 +1323,7 @@ attn_prefill_kernel(const AttnArgs a) {
   auto general = [&](int S, int t, bool issued) {
     if (!issued && t + 3 < ntiles) issue((S + 3) % kPreSlots, t + 3);
     const char* kt = slot(S);
-    const int ts = kPreKeys * t;
+    const int ts = k0 + kPreKeys * t;
     if (t < nfull)
       wa.template tile_general<Tile, false>(sl, kt, kt + Tile::BYTES, ts, kend);
     else if (ts < kend)
@@ -1264,8 +1356,14 @@ attn_prefill_kernel(const AttnArgs a) {
   float ltot[NM];
   wa.row_sums(ltot);
 #pragma unroll
-  for (int s = 0; s < NM; ++s)
-    if (wa.mval[s]) wa.store_final_blocks(a, s, qs + q0 + wa.mq[s], ltot[s]);
+  for (int s = 0; s < NM; ++s) {
+    if (!wa.mval[s]) continue;
+    if (prefix)
+      wa.store_partial_blocks(a, s, static_cast<int64_t>(pbase) + static_cast<int64_t>(q0 + wa.mq[s]) * pstride,
+                              wa.mh[s] - kvh * a.G, ltot[s]);
+    else
+      wa.store_final_blocks(a, s, qs + q0 + wa.mq[s], ltot[s]);
+  }
 }
 
 // ----------------------------------------------------------- VALU kernel --
@@ -1523,22 +1621,88 @@ constexpr int64_t kMixSlack = 2;
 // or -1, partial index).  Per split segment two int4: (query token, kv head,
 // parts, first partial index) and zeros.  Returns false when a count does not
 // fit its 16-bit field.
+// Shared prefixes: runs of at least kMinPrefixRows consecutive decode rows
+// (one query each, consecutive query tokens) whose block tables start with
+// the same blocks, over at least kMinPrefixKeys keys that precede every
+// row's own last key.  Such a run's prefix keys are attended once for all its
+// queries (prefill-kernel units, cut into key splits of at least
+// kMinSplitKeys), and each row's decode segment covers only its own keys.
+constexpr int64_t kMinPrefixRows = 4;
+constexpr int64_t kMinPrefixKeys = 256;
+constexpr int64_t kMinSplitKeys = 128;
+
+struct PrefixGroup {
+  int64_t r0, nrows, keys;  // rows [r0, r0 + nrows) share keys [0, keys)
+};
+
+// kend[r]: visible keys of decode row r (-1 for other rows).
+static std::vector<PrefixGroup> find_prefix_groups(const int32_t* q_starts, const int32_t* bt, int64_t bt_stride,
+                                                   int64_t bs, int64_t rows, const std::vector<int64_t>& kend) {
+  std::vector<PrefixGroup> out;
+  for (int64_t r = 0; r < rows;) {
+    if (kend[r] < 1 || !bt) {
+      ++r;
+      continue;
+    }
+    // Blocks wholly before row r's last key.
+    int64_t lcp = std::min<int64_t>(bt_stride, (kend[r] - 1) / bs);
+    int64_t e = r + 1;
+    while (e < rows && kend[e] >= 1 && q_starts[e] == q_starts[e - 1] + 1) {
+      const int64_t lim = std::min<int64_t>(lcp, (kend[e] - 1) / bs);
+      int64_t l = 0;
+      while (l < lim && bt[r * bt_stride + l] == bt[e * bt_stride + l]) ++l;
+      if (l * bs < kMinPrefixKeys) break;
+      lcp = l;
+      ++e;
+    }
+    const int64_t keys = lcp * bs / kPreKeys * kPreKeys;
+    if (e - r >= kMinPrefixRows && keys >= kMinPrefixKeys) {
+      out.push_back(PrefixGroup{r, e - r, keys});
+      r = e;
+    } else {
+      ++r;
+    }
+  }
+  return out;
+}
+
 static bool plan_decode(const int32_t* q_lens, const int32_t* k_lens, const int32_t* q_offs,
                         const int32_t* q_starts, const int32_t* bt, int64_t bt_stride, int64_t bs,
                         int64_t rows, int64_t Hkv, bool causal, int W, int64_t groups,
-                        int64_t given_pt, int64_t slice_bytes, std::vector<int4>& dec,
-                        std::vector<int4>& mrg, int64_t& partials) {
+                        int64_t given_pt, int64_t slice_bytes, int64_t prefix_queries, std::vector<int4>& dec,
+                        std::vector<int4>& mrg, std::vector<int4>& pfx, int64_t& partials) {
   dec.clear();
   mrg.clear();
+  pfx.clear();
   partials = 0;
   std::vector<int64_t> kend(rows, -1);
-  int64_t total = 0;
   for (int64_t r = 0; r < rows; ++r) {
     if (q_lens[r] != 1) continue;
     const int64_t klen = k_lens[r], off = q_offs[r];
     kend[r] = std::max<int64_t>(causal ? std::min(klen, off + 1) : klen, 0);
-    total += (kend[r] + 15) / 16 * Hkv;
   }
+  // Shared prefixes (none under fixed partitions): the rows' decode segments
+  // start after the prefix and fold in the ks partials of the prefix's key
+  // splits (kPrefixFold), which an earlier launch writes.
+  std::vector<PrefixGroup> pgroups;
+  if (given_pt == 0 && prefix_queries > 0) pgroups = find_prefix_groups(q_starts, bt, bt_stride, bs, rows, kend);
+  std::vector<int64_t> pfx_sl(rows, 0), pfx_splits(rows, 0);
+  for (const PrefixGroup& pg : pgroups) {
+    const int64_t qblocks = (pg.nrows + prefix_queries - 1) / prefix_queries;
+    // Key splits for about half a device-fill of prefix work-groups: on 256
+    // rows sharing 1024 keys (D=128, G=4), 128 units beat 256 (half the fp32
+    // partials to write and fold) and 64 (units twice as long).
+    const int64_t units = std::max<int64_t>(groups / 2, 1);
+    const int64_t want = (units + qblocks * Hkv - 1) / (qblocks * Hkv);
+    const int64_t ks = std::max<int64_t>(1, std::min<int64_t>(want, pg.keys / kMinSplitKeys));
+    for (int64_t r = pg.r0; r < pg.r0 + pg.nrows; ++r) {
+      pfx_sl[r] = pg.keys / 16;
+      pfx_splits[r] = ks;
+    }
+  }
+  int64_t total = 0;
+  for (int64_t r = 0; r < rows; ++r)
+    if (kend[r] >= 0) total += ((kend[r] + 15) / 16 - pfx_sl[r]) * Hkv;
   const int64_t target = std::max<int64_t>((total + std::max<int64_t>(groups, 1) - 1) / std::max<int64_t>(groups, 1),
                                            kMinGroupSlicesPerWave * W);
   const int64_t slack = std::max<int64_t>(2, target / 32);
@@ -1553,6 +1717,7 @@ static bool plan_decode(const int32_t* q_lens, const int32_t* k_lens, const int3
   };
   std::vector<int> seg_parts;  // parts per segment (row, kv head)
   std::vector<int> seg_row, seg_kvh;
+  std::vector<int64_t> seg_start(rows, -1);  // first segment of each decode row
   // Adds slices [s, s + rem) of segment seg (row r, kv head h) to the open
   // work-groups: whole when it is a fixed partition p, else cut at the
   // work-group loads.
@@ -1585,12 +1750,19 @@ static bool plan_decode(const int32_t* q_lens, const int32_t* k_lens, const int3
     if (kend[r] < 0) continue;
     const int64_t n = (kend[r] + 15) / 16;
     const int seg0 = static_cast<int>(seg_parts.size());
+    seg_start[r] = seg0;
     for (int64_t h = 0; h < Hkv; ++h) {
       seg_parts.push_back(0);
       seg_row.push_back(static_cast<int>(r));
       seg_kvh.push_back(static_cast<int>(h));
     }
-    if (pt_sl > 0) {
+    if (pfx_splits[r] > 0) {
+      // The row's own keys, whole, folding in the prefix's ks partials.
+      for (int64_t h = 0; h < Hkv; ++h) {
+        place(seg0 + static_cast<int>(h), r, h, pfx_sl[r], n - pfx_sl[r], kPrefixFold, false);
+        seg_parts[seg0 + h] = static_cast<int>(pfx_splits[r]);
+      }
+    } else if (pt_sl > 0) {
       // Fixed partitions, partition-major over the row's kv heads: a
       // work-group's run of partitions spans the heads, whose streaming
       // rates differ (see kMixCandidates).
@@ -1606,14 +1778,22 @@ static bool plan_decode(const int32_t* q_lens, const int32_t* k_lens, const int3
   }
   close();
 
-  bool any_cut = false;
-  for (int p : seg_parts) any_cut = any_cut || p > 1;
-  if (given_pt == 0 && any_cut) {
+  // Uncut plan: whole segments, longest first, onto the least loaded of
+  // `groups` work-groups.  Taken when the cut plan cut a segment and the
+  // uncut one is within a merge launch of balanced, and always when only
+  // fold segments (which the cut plan never cuts, closing work-groups early
+  // instead) are in the way.
+  bool any_cut = false, any_fold = false;
+  for (size_t sg = 0; sg < seg_parts.size(); ++sg) {
+    any_cut = any_cut || (seg_parts[sg] > 1 && pfx_splits[seg_row[sg]] == 0);
+    any_fold = any_fold || pfx_splits[seg_row[sg]] > 0;
+  }
+  if (given_pt == 0 && (any_cut || any_fold)) {
     const int nseg = static_cast<int>(seg_parts.size());
     std::vector<int64_t> n(nseg);
     std::vector<int> order(nseg);
     for (int sg = 0; sg < nseg; ++sg) {
-      n[sg] = (kend[seg_row[sg]] + 15) / 16;
+      n[sg] = (kend[seg_row[sg]] + 15) / 16 - pfx_sl[seg_row[sg]];
       order[sg] = sg;
     }
     std::stable_sort(order.begin(), order.end(), [&](int x, int y) { return n[x] > n[y]; });
@@ -1647,7 +1827,9 @@ static bool plan_decode(const int32_t* q_lens, const int32_t* k_lens, const int3
         std::push_heap(heap.begin(), heap.end(), std::greater<>());
       }
       auto [ld, g2] = cand[c];
-      lpt[g2].push_back(Piece{seg_row[sg], seg_kvh[sg], 0, static_cast<int>(n[sg]), 0, sg});
+      const int64_t s0 = pfx_sl[seg_row[sg]];
+      lpt[g2].push_back(Piece{seg_row[sg], seg_kvh[sg], static_cast<int>(s0), static_cast<int>(s0 + n[sg]),
+                              pfx_splits[seg_row[sg]] > 0 ? kPrefixFold : 0, sg});
       ++held[g2 * Hkv + h];
       ld += n[sg];
       lmax = std::max(lmax, ld);
@@ -1657,24 +1839,58 @@ static bool plan_decode(const int32_t* q_lens, const int32_t* k_lens, const int3
       }
     }
     const double slice_us = static_cast<double>(slice_bytes) * ng / (kDecodeRateGBs * 1e3);
-    if (static_cast<double>(lmax - target) * slice_us <= kMergeLaunchUs) {
+    if (!any_cut || static_cast<double>(lmax - target) * slice_us <= kMergeLaunchUs) {
       wgs.clear();
       for (auto& g2 : lpt)
         if (!g2.empty()) wgs.push_back(std::move(g2));
-      std::fill(seg_parts.begin(), seg_parts.end(), 1);
+      for (int sg = 0; sg < nseg; ++sg) {
+        const int64_t ks = pfx_splits[seg_row[sg]];
+        seg_parts[sg] = ks > 0 ? static_cast<int>(ks) : 1;
+      }
     }
   }
 
-  // Partial indices of split segments.
+  // Partial indices of split segments (merged by merge units) and of the
+  // prefix partials a fold segment reads.
   std::vector<int64_t> seg_base(seg_parts.size(), -1);
   for (size_t sg = 0; sg < seg_parts.size(); ++sg) {
     if (seg_parts[sg] > 32767) return false;  // bits 16-30 of a wave descriptor's first int
-    if (seg_parts[sg] > 1) {
+    if (pfx_splits[seg_row[sg]] > 0) {
+      seg_base[sg] = partials;
+      partials += seg_parts[sg];
+      if (partials > 0x7fffffff) return false;
+    } else if (seg_parts[sg] > 1) {
       seg_base[sg] = partials;
       mrg.push_back(int4{q_starts[seg_row[sg]], seg_kvh[sg], seg_parts[sg], static_cast<int>(partials)});
       mrg.push_back(int4{0, 0, 0, 0});
       partials += seg_parts[sg];
       if (partials > 0x7fffffff) return false;
+    }
+  }
+
+  // Shared-prefix units: (row holding the prefix, kv head, first key, end
+  // key), (first query token, queries, partial of the first query, partial
+  // stride): query block b of a group, kv head h, key split k.  The rows of a
+  // group have consecutive segments with ks partials each, so a block's
+  // partials lie at a fixed stride.
+  for (const PrefixGroup& pg : pgroups) {
+    const int64_t ks = pfx_splits[pg.r0];
+    const int64_t tiles = pg.keys / kPreKeys;
+    for (int64_t b = 0; b * prefix_queries < pg.nrows; ++b) {
+      const int64_t r = pg.r0 + b * prefix_queries;
+      const int64_t nq = std::min(prefix_queries, pg.nrows - b * prefix_queries);
+      for (int64_t h = 0; h < Hkv; ++h) {
+        const int64_t base = seg_base[seg_start[r] + h];
+        const int64_t stride = nq > 1 ? seg_base[seg_start[r + 1] + h] - base : 1;
+        for (int64_t i = 0; i < nq; ++i)
+          if (seg_base[seg_start[r + i] + h] != base + i * stride) return false;
+        for (int64_t k = 0; k < ks; ++k) {
+          const int64_t k0 = kPreKeys * (tiles * k / ks), k1 = kPreKeys * (tiles * (k + 1) / ks);
+          if (k1 <= k0) return false;
+          pfx.push_back(int4{static_cast<int>(pg.r0), static_cast<int>(h), static_cast<int>(k0), static_cast<int>(k1)});
+          pfx.push_back(int4{q_starts[r], static_cast<int>(nq), static_cast<int>(base + k), static_cast<int>(stride)});
+        }
+      }
     }
   }
 
@@ -1694,7 +1910,9 @@ static bool plan_decode(const int32_t* q_lens, const int32_t* k_lens, const int3
       const int nparts = seg_parts[pc.seg];
       const int n = pc.s1 - pc.s0;
       const int r = pc.row;
-      const int pidx = nparts > 1 ? static_cast<int>(seg_base[pc.seg] + pc.part) : 0;
+      const bool fold = pc.part == kPrefixFold;
+      const int pidx = fold ? static_cast<int>(seg_base[pc.seg])
+                            : (nparts > 1 ? static_cast<int>(seg_base[pc.seg] + pc.part) : 0);
       for (int j = 0; j < w[i]; ++j) {
         const int a0 = pc.s0 + static_cast<int>((static_cast<int64_t>(n) * j) / w[i]);
         const int a1 = pc.s0 + static_cast<int>((static_cast<int64_t>(n) * (j + 1)) / w[i]);
@@ -1793,9 +2011,19 @@ static AuxStream* aux_stream() {
 
 template <class TT, int D>
 static void launch_mfma(const AttnArgs& a, int waves, int64_t rows, int64_t max_q, int64_t n_dec,
-                        int64_t n_pre, int64_t n_merge, bool use_aux, hipStream_t stream) {
+                        int64_t n_pre, int64_t n_merge, int64_t n_pfx, bool use_aux, hipStream_t stream) {
+  constexpr int NM = prefill_nm(D);
+  if (a.sched && n_pfx > 0) {
+    // Shared-prefix units, the first n_pfx of the prefill section, before
+    // anything else on the caller's stream: the decode launch folds in the
+    // partials they write.
+    AttnArgs xa = a;
+    xa.sched = a.sched + 2 * n_dec;
+    hipLaunchKernelGGL((attn_prefill_kernel<TT, D, NM>), dim3(static_cast<uint32_t>(n_pfx)), dim3(64 * kPreWaves), 0,
+                       stream, xa);
+  }
   const bool dec = !a.sched || n_dec > 0;
-  const bool pre = a.sched ? n_pre > 0 : max_q >= 2;
+  const bool pre = a.sched ? n_pre > n_pfx : max_q >= 2;
   hipStream_t pre_stream = stream;
   std::unique_lock<std::mutex> lock(g_aux_mutex, std::defer_lock);
   AuxStream* aux = nullptr;
@@ -1811,13 +2039,12 @@ static void launch_mfma(const AttnArgs& a, int waves, int64_t rows, int64_t max_
     }
   }
   if (pre) {
-    constexpr int NM = prefill_nm(D);
     const int64_t qpw = kPreWaves * 16 * NM / a.G;
     const int64_t nqb = (max_q + qpw - 1) / qpw;
-    dim3 grid = a.sched ? dim3(static_cast<uint32_t>(n_pre))
+    dim3 grid = a.sched ? dim3(static_cast<uint32_t>(n_pre - n_pfx))
                         : dim3(static_cast<uint32_t>(a.Hkv * nqb), 1u, static_cast<uint32_t>(rows));
     AttnArgs pa = a;
-    if (a.sched) pa.sched = a.sched + 2 * n_dec;
+    if (a.sched) pa.sched = a.sched + 2 * (n_dec + n_pfx);
     hipLaunchKernelGGL((attn_prefill_kernel<TT, D, NM>), grid, dim3(64 * kPreWaves), 0, pre_stream, pa);
   }
   if (dec) {
@@ -1829,11 +2056,11 @@ static void launch_mfma(const AttnArgs& a, int waves, int64_t rows, int64_t max_
     } else {
       launch_decode<TT, D, 8>(a, rows, n_dec, stream);
     }
-    if (a.sched ? n_merge > 0 : a.max_parts > 1) {
-      dim3 mgrid = a.sched ? dim3(static_cast<uint32_t>(n_merge))
-                           : dim3(static_cast<uint32_t>((a.Hq * (D / 8) + 63) / 64), static_cast<uint32_t>(rows));
-      hipLaunchKernelGGL((attn_merge_kernel<TT, D>), mgrid, dim3(a.sched ? 64 * kMergeWaves : 64), 0, stream, a);
-    }
+  }
+  if (a.sched ? n_merge > 0 : dec && a.max_parts > 1) {
+    dim3 mgrid = a.sched ? dim3(static_cast<uint32_t>(n_merge))
+                         : dim3(static_cast<uint32_t>((a.Hq * (D / 8) + 63) / 64), static_cast<uint32_t>(rows));
+    hipLaunchKernelGGL((attn_merge_kernel<TT, D>), mgrid, dim3(a.sched ? 64 * kMergeWaves : 64), 0, stream, a);
   }
   if (aux) {
     // Join: the caller's stream waits for the prefill launch.  (Errors of
@@ -1866,7 +2093,8 @@ extern "C" int64_t kvhot_paged_attention_schedule(
     int64_t num_rows, int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim,
     int64_t block_size, int64_t partition_tokens, int is_causal, int dtype,
     int32_t* units, int64_t capacity_units, int64_t* num_decode_units,
-    int64_t* num_prefill_units, int64_t* num_merge_units, int64_t* workspace_bytes) {
+    int64_t* num_prefill_units, int64_t* num_merge_units, int64_t* workspace_bytes,
+    int64_t* num_prefix_units) {
   clear_error();
   if (num_rows < 0 || num_q_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0 ||
       block_size <= 0 || partition_tokens < 0 || num_q_heads % num_kv_heads != 0 ||
@@ -1886,18 +2114,20 @@ extern "C" int64_t kvhot_paged_attention_schedule(
     max_q = std::max<int64_t>(max_q, q_lens[r]);
     max_k = std::max<int64_t>(max_k, k_lens[r]);
   }
-  std::vector<int4> dec, pre, mrg;
+  std::vector<int4> dec, pre, mrg, pfx;
   int64_t partials = 0;
   const Plan pl = make_plan(num_rows, max_q, max_k, num_q_heads, num_kv_heads, head_dim,
                             block_size, partition_tokens, dtype);
   if (pl.mfma) {
     const int64_t G = num_q_heads / num_kv_heads;
     const int64_t groups = resident_decode_waves(dtype, head_dim, pl.waves, G) / pl.waves;
+    const int64_t prefix_queries = kPreWaves * 16 * prefill_nm(head_dim) / G;  // per prefill work-group
     if (plan_decode(q_lens, k_lens, q_pos_offsets, q_starts, block_table, bt_row_stride, block_size,
                     num_rows, num_kv_heads, is_causal != 0, pl.waves, groups, partition_tokens,
-                    32 * head_dim * dtype_size(dtype), dec, mrg, partials)) {
+                    32 * head_dim * dtype_size(dtype), prefix_queries, dec, mrg, pfx, partials)) {
       plan_prefill(q_lens, k_lens, q_pos_offsets, num_rows, num_kv_heads, G, head_dim,
                    is_causal != 0, pre);
+      pre.insert(pre.begin(), pfx.begin(), pfx.end());  // shared-prefix units first
     } else {  // counts beyond the descriptor fields: no schedule
       dec.clear();
       mrg.clear();
@@ -1912,6 +2142,7 @@ extern "C" int64_t kvhot_paged_attention_schedule(
   if (num_decode_units) *num_decode_units = n_dec;
   if (num_prefill_units) *num_prefill_units = n_pre;
   if (num_merge_units) *num_merge_units = n_mrg;
+  if (num_prefix_units) *num_prefix_units = static_cast<int64_t>(pfx.size() / 2);
   if (workspace_bytes) *workspace_bytes = partials * partial_bytes(num_q_heads / num_kv_heads, head_dim);
   if (units && capacity_units >= n_dec + n_pre + n_mrg) {
     int4* out = reinterpret_cast<int4*>(units);
@@ -1936,7 +2167,7 @@ static int paged_attention_impl(
     int64_t block_size, int64_t num_blocks, float scale, int is_causal,
     int dtype, int64_t partition_tokens, const int32_t* schedule,
     int64_t num_decode_units, int64_t num_prefill_units, int64_t num_merge_units,
-    int64_t schedule_workspace_bytes, void* workspace, int64_t workspace_bytes, bool use_aux,
+    int64_t num_prefix_units, int64_t schedule_workspace_bytes, void* workspace, int64_t workspace_bytes, bool use_aux,
     void* stream) {
   clear_error();
   const int64_t es = dtype_size(dtype);
@@ -1987,8 +2218,10 @@ static int paged_attention_impl(
   const int64_t n_dec = schedule ? num_decode_units : 0;
   const int64_t n_pre = schedule ? num_prefill_units : 0;
   const int64_t n_mrg = schedule ? num_merge_units : 0;
+  const int64_t n_pfx = schedule ? num_prefix_units : 0;
   if (schedule && (n_dec < 0 || n_pre < 0 || n_mrg < 0 || n_dec > 0x7fffffff ||
-                   n_pre > 0x7fffffff || n_mrg > 0x7fffffff || schedule_workspace_bytes < 0))
+                   n_pre > 0x7fffffff || n_mrg > 0x7fffffff || schedule_workspace_bytes < 0 ||
+                   n_pfx < 0 || n_pfx > n_pre))
     return set_error(KVHOT_EINVAL, "paged_attention: bad schedule unit counts");
   a.sched = reinterpret_cast<const int4*>(schedule);
   a.merge_units = (schedule && n_mrg > 0) ? a.sched + 2 * (n_dec + n_pre) : nullptr;
@@ -2017,9 +2250,10 @@ static int paged_attention_impl(
   }
   if (pl.mfma) {
     const int64_t pb = partial_bytes(a.G, head_dim);
-    if (schedule && n_mrg > 0 && schedule_workspace_bytes < pb)
-      return set_error(KVHOT_EINVAL, "paged_attention: a schedule with merge units needs partials");
-    const int64_t need = schedule ? (n_mrg > 0 ? schedule_workspace_bytes : 0) : pl.workspace_bytes(a.G, head_dim);
+    if (schedule && (n_mrg > 0 || n_pfx > 0) && schedule_workspace_bytes < pb)
+      return set_error(KVHOT_EINVAL, "paged_attention: a schedule with merge or prefix units needs partials");
+    const int64_t need = schedule ? (n_mrg > 0 || n_pfx > 0 ? schedule_workspace_bytes : 0)
+                                  : pl.workspace_bytes(a.G, head_dim);
     if (need > 0) {
       if (!workspace || workspace_bytes < need)
         return set_error(KVHOT_EWORKSPACE,
@@ -2032,7 +2266,8 @@ static int paged_attention_impl(
       a.part_tokens = pl.part_tokens;
       a.max_parts = pl.max_parts;
     }
-#define KVHOT_MFMA(TT, DD) launch_mfma<TT, DD>(a, pl.waves, num_rows, max_q_len, n_dec, n_pre, n_mrg, use_aux, s)
+#define KVHOT_MFMA(TT, DD) \
+  launch_mfma<TT, DD>(a, pl.waves, num_rows, max_q_len, n_dec, n_pre, n_mrg, n_pfx, use_aux, s)
     if (dtype == KVHOT_BF16) {
       if (head_dim == 64) KVHOT_MFMA(BF16, 64);
       else if (head_dim == 128) KVHOT_MFMA(BF16, 128);
@@ -2071,13 +2306,13 @@ extern "C" int kvhot_paged_attention(
     int64_t block_size, int64_t num_blocks, float scale, int is_causal,
     int dtype, int64_t partition_tokens, const int32_t* schedule,
     int64_t num_decode_units, int64_t num_prefill_units, int64_t num_merge_units,
-    int64_t schedule_workspace_bytes, void* workspace, int64_t workspace_bytes, void* stream) {
+    int64_t num_prefix_units, int64_t schedule_workspace_bytes, void* workspace, int64_t workspace_bytes, void* stream) {
   return paged_attention_impl(q, q_strides, k_cache, k_cache_strides, v_cache, v_cache_strides, out, out_strides,
                               lse, lse_strides, block_table, bt_row_stride, q_lens, k_lens, q_starts,
                               q_pos_offsets, num_rows, total_query, max_q_len, max_k_len, num_q_heads,
                               num_kv_heads, head_dim, block_size, num_blocks, scale, is_causal, dtype,
                               partition_tokens, schedule, num_decode_units, num_prefill_units, num_merge_units,
-                              schedule_workspace_bytes, workspace, workspace_bytes, true, stream);
+                              num_prefix_units, schedule_workspace_bytes, workspace, workspace_bytes, true, stream);
 }
 
 // ------------------------------------------------------------ no-alloc --
@@ -2128,7 +2363,7 @@ extern "C" int kvhot_paged_attention_noalloc(
     int64_t block_size, int64_t num_blocks, float scale, int is_causal,
     int dtype, int64_t partition_tokens, const int32_t* schedule,
     int64_t num_decode_units, int64_t num_prefill_units, int64_t num_merge_units,
-    int64_t schedule_workspace_bytes, void* stream) {
+    int64_t num_prefix_units, int64_t schedule_workspace_bytes, void* stream) {
   clear_error();
   int64_t need = 0;
   if (schedule) {
@@ -2152,6 +2387,6 @@ extern "C" int kvhot_paged_attention_noalloc(
                               q_pos_offsets, num_rows, total_query, max_q_len, max_k_len, num_q_heads,
                               num_kv_heads, head_dim, block_size, num_blocks, scale, is_causal, dtype,
                               partition_tokens, schedule, num_decode_units, num_prefill_units, num_merge_units,
-                              schedule_workspace_bytes, ws, need > 0 ? int64_t{KVHOT_NOALLOC_SCRATCH_BYTES} : 0,
+                              num_prefix_units, schedule_workspace_bytes, ws, need > 0 ? int64_t{KVHOT_NOALLOC_SCRATCH_BYTES} : 0,
                               false, stream);
 }

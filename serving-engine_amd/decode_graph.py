@@ -109,7 +109,7 @@ class DecodeStepGraph:
         r, mb = self.r, self.max_blocks
         hq, hkv, d, bs, pt, causal, dt = self.shape
         lib = _lib.load()
-        cnt = [ctypes.c_int64(0) for _ in range(4)]
+        cnt = [ctypes.c_int64(0) for _ in range(5)]  # decode, prefill, merge, workspace, prefix
         outs = tuple(ctypes.byref(c) for c in cnt)
         base = a.ctypes.data  # q_lens, k_lens, q_starts, q_pos_offsets, block table: int32 views of `a`
         args = (base, base + 4 * r, base + 8 * r, base + 12 * r, base + 16 * r, mb, r, hq, hkv, d, bs, pt,
@@ -136,13 +136,13 @@ class DecodeStepGraph:
         self.tokens.copy_(self.logits.argmax(-1))
 
     def _record(self, units, counts):
-        n_dec, n_pre, n_mrg, need = counts
+        n_dec, n_pre, n_mrg, need, n_pfx = counts
         self._units_dev = units.to(self.device, non_blocking=True)
         # The attention calls find their launch list here (no host copies
         # are read once it is present).
         self.meta["host_q_lens"] = self._host[0].numpy()[: self.r]
         self.meta["_schedules"] = {
-            schedule_key(self.device, *self.shape): (self._units_dev, n_dec, n_pre, n_mrg, need)}
+            schedule_key(self.device, *self.shape): (self._units_dev, n_dec, n_pre, n_mrg, need, n_pfx)}
         stream = torch.cuda.current_stream(self.device)
         saved = self.tokens.clone()
         # One eager pass on a side stream first (lazy library set-up and

@@ -64,8 +64,8 @@ def schedule_key(device, hq, hkv, d, bs, pt, causal, dtype):
 
 
 def _schedule(metadata, device, hq, hkv, d, bs, pt, causal, dtype):
-    """(device units, n_decode, n_prefill, n_merge, workspace bytes) of
-    kvhot_paged_attention_schedule for this step, built once per attention
+    """(device units, n_decode, n_prefill, n_merge, workspace bytes, n_prefix)
+    of kvhot_paged_attention_schedule for this step, built once per attention
     shape from the host copies of the metadata and cached in the metadata
     dict; None without host copies."""
     host_q = metadata.get("host_q_lens")
@@ -80,7 +80,8 @@ def _schedule(metadata, device, hq, hkv, d, bs, pt, causal, dtype):
     host_qs = metadata["host_q_starts"]
     host_bt = metadata["host_block_table"]
     lib = _lib.load()
-    counts = [ctypes.c_int64(0) for _ in range(4)]  # decode, prefill, merge units; workspace bytes
+    # decode, prefill, merge units; workspace bytes; shared-prefix units
+    counts = [ctypes.c_int64(0) for _ in range(5)]
     args = (host_q.ctypes.data, host_k.ctypes.data, host_qs.ctypes.data, host_off.ctypes.data,
             host_bt.ctypes.data if host_bt.size else None, host_bt.shape[1] if host_bt.ndim == 2 else 0,
             len(host_q), hq, hkv, d, bs, pt, 1 if causal else 0, dtype)
@@ -170,9 +171,9 @@ def paged_flash_attention(q, k_cache, v_cache, metadata, num_q_heads, num_kv_hea
     plan = _schedule(metadata, device, num_q_heads, num_kv_heads, head_dim, block_size, pt,
                      is_causal, dtype)
     if plan is not None:
-        sched, n_dec, n_pre, n_mrg, need = plan
+        sched, n_dec, n_pre, n_mrg, need, n_pfx = plan
     else:
-        sched, n_dec, n_pre, n_mrg = None, 0, 0, 0
+        sched, n_dec, n_pre, n_mrg, n_pfx = None, 0, 0, 0, 0
         need = lib.kvhot_paged_attention_workspace_bytes(
             num_rows, total_query, max_q, max_k, num_q_heads, num_kv_heads, head_dim,
             block_size, pt, dtype)
@@ -190,7 +191,7 @@ def paged_flash_attention(q, k_cache, v_cache, metadata, num_q_heads, num_kv_hea
         metadata["q_starts"].data_ptr(), metadata["q_pos_offsets"].data_ptr(),
         num_rows, total_query, max_q, max_k, num_q_heads, num_kv_heads, head_dim,
         block_size, num_blocks, float(scale), 1 if is_causal else 0, dtype, pt,
-        sched.data_ptr() if sched is not None else None, n_dec, n_pre, n_mrg,
+        sched.data_ptr() if sched is not None else None, n_dec, n_pre, n_mrg, n_pfx,
         need if sched is not None else 0,
         ws.data_ptr() if ws is not None else None, ws.numel() if ws is not None else 0,
         stream)

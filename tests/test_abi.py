@@ -73,7 +73,7 @@ def test_attention_rejects_bad_arguments(lib):
     q3, c4, l2 = _i64(4096, 128, 1), _i64(16384, 1024, 128, 1), _i64(32, 1)
     f = FAKE
     args = [f, q3, f, c4, f, c4, f, q3, f, l2, f, 8, f, f, f, f,
-            4, 4, 1, 100, 32, 8, 128, 16, 64, 0.1, 1, 2, 64, None, 0, 0, 0, 0, None, 0, None]
+            4, 4, 1, 100, 32, 8, 128, 16, 64, 0.1, 1, 2, 64, None, 0, 0, 0, 0, 0, None, 0, None]
     bad = list(args)
     bad[20] = 30  # Hq not a multiple of Hkv
     assert lib.kvhot_paged_attention(*bad) == -1
@@ -100,20 +100,28 @@ def test_attention_rejects_bad_arguments(lib):
 def test_attention_checks_the_schedule_workspace(lib):
     """A schedule's reported workspace size comes with it: a workspace
     shorter than that is KVHOT_EWORKSPACE before any launch, and a schedule
-    with merge units must report room for its partials."""
+    with merge or shared-prefix units must report room for its partials."""
     q3, c4, l2 = _i64(4096, 128, 1), _i64(16384, 1024, 128, 1), _i64(32, 1)
     f = FAKE
     need = 10 * 4 * (128 + 1) * 4  # 10 partials of 4 query heads x (128 + 1) floats
     # one 16-wave decode work-group and one merge unit
     args = [f, q3, f, c4, f, c4, f, q3, f, l2, f, 8, f, f, f, f,
-            4, 4, 1, 100, 32, 8, 128, 16, 64, 0.1, 1, 2, 0, f, 16, 0, 1, need, f, need - 1, None]
+            4, 4, 1, 100, 32, 8, 128, 16, 64, 0.1, 1, 2, 0, f, 16, 0, 1, 0, need, f, need - 1, None]
     assert lib.kvhot_paged_attention(*args) == -3
     assert str(need).encode() in lib.kvhot_last_error()
     bad = list(args)
-    bad[33] = 100  # less than one partial
+    bad[34] = 100  # less than one partial
     assert lib.kvhot_paged_attention(*bad) == -1
-    bad[33] = -1
+    bad[34] = -1
     assert lib.kvhot_paged_attention(*bad) == -1
+    # shared-prefix units are counted among the prefill units, and need partials too
+    pfx = list(args)
+    pfx[31:35] = [2, 0, 3, need]  # more prefix units than prefill units
+    assert lib.kvhot_paged_attention(*pfx) == -1
+    pfx[31:35] = [2, 0, 2, 100]
+    assert lib.kvhot_paged_attention(*pfx) == -1
+    pfx[31:35] = [2, 0, -1, need]
+    assert lib.kvhot_paged_attention(*pfx) == -1
 
 
 @no_gpu
@@ -125,13 +133,13 @@ def test_noalloc_rejects_calls_beyond_its_scratch(lib):
     f = FAKE
     # no schedule: 64 rows of up to 65536 keys in 32-key partitions -> 64 x 8 x 2048 partials of 2064 bytes
     args = [f, q3, f, c4, f, c4, f, q3, f, l2, f, 4096, f, f, f, f,
-            64, 64, 1, 65536, 32, 8, 128, 16, 1 << 20, 0.1, 1, 2, 32, None, 0, 0, 0, 0, None]
+            64, 64, 1, 65536, 32, 8, 128, 16, 1 << 20, 0.1, 1, 2, 32, None, 0, 0, 0, 0, 0, None]
     assert lib.kvhot_paged_attention_noalloc(*args) == -3
     msg = lib.kvhot_last_error()
     assert str(64 * 8 * 2048 * 4 * 129 * 4).encode() in msg and b"33554432" in msg
     # a schedule whose merge units need one byte more than the scratch
     sched = list(args)
-    sched[29:34] = [f, 16, 0, 1, (32 << 20) + 1]
+    sched[29:35] = [f, 16, 0, 1, 0, (32 << 20) + 1]
     assert lib.kvhot_paged_attention_noalloc(*sched) == -3
     # invalid sizes are reported as such
     bad = list(args)
@@ -151,18 +159,25 @@ def test_workspace_bytes(lib):
     assert lib.kvhot_paged_attention_workspace_bytes(64, 64, 1, 2048, 30, 8, 128, 16, 256, 2) < 0
 
 
-def _schedule(lib, q_lens, k_lens, offs, hq=32, hkv=8, d=128, pt=0, causal=1, dtype=2):
+def _schedule(lib, q_lens, k_lens, offs, hq=32, hkv=8, d=128, pt=0, causal=1, dtype=2, bt=None,
+              prefix=False):
     """Runs the host planner; returns (decode descriptors as dicts, prefill
-    units, merge units, workspace bytes, query token of each row)."""
+    units, merge units, workspace bytes, query token of each row), and with
+    prefix=True also the number of shared-prefix units (the first ones of
+    the prefill units).  Without `bt`, row r's block j is 1000 + r*mb + j
+    (no blocks shared)."""
     import numpy as np
 
     q = np.asarray(q_lens, np.int32)
     k = np.asarray(k_lens, np.int32)
     o = np.asarray(offs, np.int32)
     qs = np.concatenate([[0], np.cumsum(q)[:-1]]).astype(np.int32)
-    mb = max(-(-int(x) // 16) for x in k)
-    bt = (np.arange(len(q) * mb, dtype=np.int32).reshape(len(q), mb) + 1000)  # block ids 1000 + r*mb + j
-    cnt = [ctypes.c_int64() for _ in range(4)]
+    if bt is None:
+        mb = max(-(-int(x) // 16) for x in k)
+        bt = (np.arange(len(q) * mb, dtype=np.int32).reshape(len(q), mb) + 1000)
+    bt = np.ascontiguousarray(bt, np.int32)
+    mb = bt.shape[1]
+    cnt = [ctypes.c_int64() for _ in range(5)]
     outs = tuple(ctypes.byref(c) for c in cnt)
     head = (q.ctypes.data, k.ctypes.data, qs.ctypes.data, o.ctypes.data, bt.ctypes.data, mb, len(q), hq, hkv,
             d, 16, pt, causal, dtype)
@@ -170,18 +185,21 @@ def _schedule(lib, q_lens, k_lens, offs, hq=32, hkv=8, d=128, pt=0, causal=1, dt
     units = np.zeros((max(total, 0), 8), np.int32)
     got = lib.kvhot_paged_attention_schedule(*head, units.ctypes.data, total, *outs)
     assert got == total
-    nd, npf, nm, ws = (c.value for c in cnt)
-    assert nd + npf + nm == total
+    nd, npf, nm, ws, npx = (c.value for c in cnt)
+    assert nd + npf + nm == total and 0 <= npx <= npf
     dec = []
     for x, y, s0, s1, qtok, kend, first, pidx in units[:nd].tolist():
         if x < 0:
             dec.append(None)
             continue
-        row, nparts, kvh, part = x & 0xFFFF, x >> 16, y & 0xFFFF, y >> 16
+        row, nparts, kvh, part = x & 0xFFFF, x >> 16, y & 0xFFFF, (y >> 16) & 0xFFFF
         # each descriptor carries its row's query token, visible keys and first block
         assert qtok == qs[row] and kend == min(k[row], o[row] + 1)
-        assert first == (1000 + row * mb + s0 if s0 < s1 else -1)
+        assert first == (bt[row, s0] if s0 < s1 else -1)
         dec.append(dict(row=row, nparts=nparts, kvh=kvh, part=part, s0=s0, s1=s1, pidx=pidx))
+    if prefix:
+        return dec, units[nd:nd + npf], units[nd + npf:], ws, qs, npx
+    assert npx == 0
     return dec, units[nd:nd + npf], units[nd + npf:], ws, qs
 
 
@@ -348,7 +366,7 @@ def test_schedule_limits_partitions_per_row(lib):
         qs = np.zeros(1, np.int32)
         mb = -(-int(k[0]) // 16)
         bt = np.arange(mb, dtype=np.int32).reshape(1, mb)
-        cnt = [ctypes.c_int64() for _ in range(4)]
+        cnt = [ctypes.c_int64() for _ in range(5)]
         total = lib.kvhot_paged_attention_schedule(
             q.ctypes.data, k.ctypes.data, qs.ctypes.data, o.ctypes.data, bt.ctypes.data, mb, 1, 32, 8, 128,
             16, 32, 1, 2, None, 0, *(ctypes.byref(c) for c in cnt))
@@ -362,3 +380,131 @@ def test_schedule_empty_for_vector_path(lib):
     # fp32 runs the VALU kernel: no launch list
     dec, pre, merge, ws, _ = _schedule(lib, [1, 1], [100, 50], [99, 49], dtype=0)
     assert len(dec) == 0 and len(pre) == 0 and len(merge) == 0 and ws == 0
+
+
+FOLD = 0x8000  # part field of a decode segment that folds in shared-prefix partials
+
+
+def test_schedule_shared_prefix_units(lib):
+    """Decode rows whose block tables start with the same blocks: the common
+    prefix is attended by prefix units (the first units of the prefill
+    section) once per query block, cut into key splits that tile it; each
+    row's decode segment starts after the prefix, is never cut across
+    work-groups, and names the partials the splits write for its query,
+    which no other unit uses.  Rows below the group size, or a prefill row
+    between decode rows, get no prefix."""
+    import numpy as np
+
+    hq, hkv, d, G = 32, 8, 128, 4
+    pq = 8 * 16 * 2 // G  # queries per prefix unit at D=128: 64
+    q_lens = [40] + [1] * 70 + [1] * 2 + [1] * 3
+    k_lens = [100] + [1500 + 37 * i for i in range(70)] + [900, 2100] + [800, 810, 820]
+    offs = [60] + [k - 1 for k in k_lens[1:]]
+    rows = len(q_lens)
+    mb = max(-(-k // 16) for k in k_lens)
+    bt = np.arange(rows * mb, dtype=np.int32).reshape(rows, mb) + 1000
+    bt[1:71, :70] = 500000 + np.arange(70)  # 70 shared blocks: 1120 keys
+    bt[73:76, :40] = 600000 + np.arange(40)  # only three rows: no group
+    dec, pre, merge, ws, qs, npx = _schedule(lib, q_lens, k_lens, offs, hq=hq, hkv=hkv, d=d, bt=bt, prefix=True)
+    assert npx > 0 and npx % (2 * hkv) == 0  # two query blocks of the 70 rows, every kv head
+    ks = npx // (2 * hkv)
+    assert 1 <= ks <= 1120 // 128
+    pb = G * (d + 1) * 4
+    nparts_total = ws // pb
+    assert ws == nparts_total * pb
+    # decode segments of every (row, kv head)
+    segs = {}
+    for g0 in range(0, len(dec), 16):
+        for wv in dec[g0:g0 + 16]:
+            if wv is not None:
+                segs.setdefault((wv["row"], wv["kvh"]), []).append((g0, wv))
+    pidx_of = {}
+    for (row, h), waves in segs.items():
+        waves.sort(key=lambda t: t[1]["s0"])
+        n = -(-k_lens[row] // 16)
+        assert waves[-1][1]["s1"] == n
+        assert all(a[1]["s1"] == b[1]["s0"] for a, b in zip(waves, waves[1:]))
+        if 1 <= row <= 70:
+            assert waves[0][1]["s0"] == 70  # the tail only
+            assert len({g for g, _ in waves}) == 1, "a folding segment cut across work-groups"
+            assert {w["part"] for _, w in waves} == {FOLD}
+            assert {w["nparts"] for _, w in waves} == {ks}
+            (pidx,) = {w["pidx"] for _, w in waves}
+            pidx_of[(row, h)] = pidx
+        else:
+            assert waves[0][1]["s0"] == 0
+            assert all(w["part"] != FOLD for _, w in waves)
+    assert len(pidx_of) == 70 * hkv
+    # prefix units: (row, kv head, k0, k1), (query token, queries, partial, stride)
+    pfx = pre[:npx].reshape(-1, 2, 4)
+    rest = pre[npx:].reshape(-1, 2, 4)  # the prefill row's units follow
+    assert len(rest) == hkv and all(u[0][0] == 0 and not u[1].any() for u in rest)
+    tiles = {}
+    written = []
+    for (r0, h, k0, k1), (qtok, nq, base, stride) in pfx.tolist():
+        assert r0 == 1 and 0 <= k0 < k1 <= 1120 and k0 % 32 == 0 and k1 % 32 == 0
+        first = qtok - int(qs[1])
+        assert first % pq == 0 and nq == min(pq, 70 - first)
+        tiles.setdefault((first, h), []).append((k0, k1, base))
+        for i in range(nq):
+            written.append((first + 1 + i, h, base + i * stride))
+    for (first, h), ranges in tiles.items():
+        ranges.sort()
+        assert ranges[0][0] == 0 and ranges[-1][1] == 1120 and len(ranges) == ks
+        assert all(a[1] == b[0] for a, b in zip(ranges, ranges[1:]))
+    # split k of (row, h) writes partial pidx + k: exactly the ones the decode segment folds
+    by_row = {}
+    for row, h, p in written:
+        by_row.setdefault((row, h), []).append(p)
+    assert set(by_row) == set(pidx_of)
+    for key, ps in by_row.items():
+        assert sorted(ps) == list(range(pidx_of[key], pidx_of[key] + ks))
+    fold_parts = [p for ps in by_row.values() for p in ps]
+    merge_parts = [b + j for _, _, n, b, *_ in merge.tolist() for j in range(n)]
+    allp = fold_parts + merge_parts
+    assert len(set(allp)) == len(allp) and max(allp) < nparts_total
+    assert not any(q - int(qs[1]) in range(70) for q, *_ in merge.tolist())
+
+
+def test_schedule_shared_prefix_needs_enough_keys(lib):
+    """Shared blocks covering fewer than 256 keys before a row's last key,
+    or a fixed partition size, leave the rows without prefix units."""
+    import numpy as np
+
+    k_lens = [1000] * 8
+    bt = np.arange(8 * 63, dtype=np.int32).reshape(8, 63) + 1000
+    bt[:, :15] = 7  # 240 shared keys
+    *_, npx = _schedule(lib, [1] * 8, k_lens, [k - 1 for k in k_lens], bt=bt, prefix=True)
+    assert npx == 0
+    bt[:, :16] = 7  # 256
+    *_, npx = _schedule(lib, [1] * 8, k_lens, [k - 1 for k in k_lens], bt=bt, prefix=True)
+    assert npx > 0
+    *_, npx = _schedule(lib, [1] * 8, k_lens, [k - 1 for k in k_lens], bt=bt, prefix=True, pt=256)
+    assert npx == 0
+    # the prefix must end before every row's last key: a 257-key row caps it at 256
+    k_lens = [1000] * 7 + [257]
+    bt[:, :62] = 7
+    *_, npx = _schedule(lib, [1] * 8, k_lens, [k - 1 for k in k_lens], bt=bt, prefix=True)
+    assert npx > 0
+
+
+def test_schedule_shared_prefix_stays_within_one_device_fill(lib):
+    """256 rows sharing 64 blocks with private tails of 64..512 keys (the
+    prefix-sharing workload's shape): the tails, which are never cut, are
+    packed into at most one device-full of decode work-groups (256 of 16
+    waves where no device is visible) with balanced loads."""
+    import numpy as np
+
+    rng = np.random.default_rng(4)
+    tails = rng.integers(64, 512, size=256, endpoint=True)
+    k_lens = [1024 + int(t) for t in tails]
+    mb = max(-(-k // 16) for k in k_lens)
+    bt = np.arange(256 * mb, dtype=np.int32).reshape(256, mb) + 1000
+    bt[:, :64] = 7 + np.arange(64)
+    dec, pre, merge, ws, qs, npx = _schedule(lib, [1] * 256, k_lens, [k - 1 for k in k_lens], bt=bt, prefix=True)
+    assert npx > 0 and len(merge) == 0
+    assert len(dec) <= 4096 and len(dec) % 16 == 0
+    loads = [sum(w["s1"] - w["s0"] for w in dec[g:g + 16] if w is not None) for g in range(0, len(dec), 16)]
+    total = sum(-(-k // 16) - 64 for k in k_lens) * 8
+    assert sum(loads) == total
+    assert max(loads) <= total / len(loads) + 32  # within one tail of the mean

@@ -418,6 +418,51 @@ def test_shapes_mixed_batch(cuda, sea, wl, hq, hkv, d, dtype):
     assert bool(plans) == mfma_shape(hq, hkv, d, dtype), (hq, hkv, d, dtype)
 
 
+def shared_custom(wl, spec, share, hq, hkv, d, dtype, seed=5):
+    """custom() whose rows share leading blocks: share = [(first row, rows,
+    blocks)], each such run of rows reading the same first `blocks` physical
+    blocks."""
+    w = custom(wl, spec, hq, hkv, d, dtype, seed=seed)
+    n = w.num_blocks
+    extra = sum(nb for _, _, nb in share)
+    perm = np.random.default_rng(seed + 1).permutation(extra) + n
+    k = 0
+    for r0, nrows, nb in share:
+        common = perm[k:k + nb].astype(np.int64)
+        k += nb
+        for x in w.rows[r0:r0 + nrows]:
+            assert x.q_pos_offset >= nb * 16  # the row's own token lands past the shared blocks
+            x.block_table = np.concatenate([common, x.block_table[nb:]])
+    w.num_blocks = n + extra
+    return w
+
+
+# a prefill chunk, 70 decode rows sharing 40 blocks (640 keys; one with a
+# single key past them), two rows of their own, four sharing too few keys
+SHARED = ([(24, 200, 176)] + [(1, 641 + 23 * i, 640 + 23 * i) for i in range(70)]
+          + [(1, 900, 899), (1, 1500, 1499)] + [(1, 300 + i, 299 + i) for i in range(4)])
+SHARED_RUNS = [(1, 70, 40), (73, 4, 15)]
+
+
+@pytest.mark.parametrize("hq,hkv,d,dtype", [
+    (32, 8, 128, torch.bfloat16), (8, 8, 128, torch.bfloat16), (32, 8, 64, torch.bfloat16),
+    (16, 4, 256, torch.bfloat16), (64, 4, 128, torch.float16), (16, 8, 128, torch.bfloat16),
+])
+def test_shared_prefix_shapes(cuda, sea, wl, hq, hkv, d, dtype):
+    """Decode rows sharing their leading blocks: the prefix keys are attended
+    once by prefix units and folded into each row's decode; the whole batch
+    (prefill chunk and unshared rows included) matches the oracle."""
+    w = shared_custom(wl, SHARED, SHARED_RUNS, hq, hkv, d, dtype)
+    announce(f"shared prefix Hq={hq} Hkv={hkv} D={d} {dtype}")
+    T = wl.make_tensors(w, cuda)
+    ref_o, ref_l = oracle_step(w, T)
+    meta = wl.metadata_tensors(w, cuda)
+    o, l = hip_step(sea, wl, w, T, meta=meta)
+    assert_attention(w, o, l, ref_o, ref_l)
+    (plan,) = [p for p in meta["_schedules"].values() if p is not None]
+    assert plan[5] > 0  # prefix units ran
+
+
 def test_non_causal(cuda, sea, wl):
     w = custom(wl, [(5, 40, 0), (1, 100, 50), (33, 33, 0)], 32, 8, 128, torch.bfloat16)
     announce("non-causal")

@@ -58,10 +58,10 @@ def attention(sea, lib, w, T, meta, pt, scheduled, noalloc):
     if scheduled:
         plan = pak._schedule(meta, device, hq, hkv, d, 16, pt, True, dtype)
         assert plan is not None
-        sched, n_dec, n_pre, n_mrg, need = plan
+        sched, n_dec, n_pre, n_mrg, need, n_pfx = plan
         assert n_pre > 0 and n_mrg > 0  # prefill beside decode, and partials to merge
     else:
-        sched, n_dec, n_pre, n_mrg = None, 0, 0, 0
+        sched, n_dec, n_pre, n_mrg, n_pfx = None, 0, 0, 0, 0
         need = lib.kvhot_paged_attention_workspace_bytes(rows, total, max_q, max_k, hq, hkv, d, 16, pt, dtype)
         assert need > 0
     bt = meta["block_table"]
@@ -71,7 +71,7 @@ def attention(sea, lib, w, T, meta, pt, scheduled, noalloc):
               meta["q_lens"].data_ptr(), meta["k_lens"].data_ptr(), meta["q_starts"].data_ptr(),
               meta["q_pos_offsets"].data_ptr(), rows, total, max_q, max_k, hq, hkv, d, 16, kc.shape[0],
               1.0 / math.sqrt(d), 1, dtype, pt, sched.data_ptr() if sched is not None else None,
-              n_dec, n_pre, n_mrg, need if sched is not None else 0]
+              n_dec, n_pre, n_mrg, n_pfx, need if sched is not None else 0]
     stream = _lib.stream_handle(device)
     if noalloc:
         status = lib.kvhot_paged_attention_noalloc(*common, stream)
