@@ -92,6 +92,31 @@ __device__ inline void dma16(__amdgpu_buffer_rsrc_t r, void* dst, int off) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr_t)dst, 16, off, 0, 0, 0);
 }
 
+// The words of the buffer descriptor block_rsrc builds: base, stride 0,
+// `bytes` records, the same flags.
+typedef uint32_t rsrc_words_t __attribute__((ext_vector_type(4)));
+__device__ inline rsrc_words_t rsrc_words(const void* base, int bytes) {
+  const uint64_t b = reinterpret_cast<uint64_t>(base);
+  return rsrc_words_t{static_cast<uint32_t>(b), static_cast<uint32_t>(b >> 32) & 0xffffu,
+                      static_cast<uint32_t>(bytes), 0x00020000u};
+}
+
+// dma16 as inline assembly.  The compiler's wait insertion treats every LDS
+// read without alias-scope metadata (the ds_read_tr builtins have none) as
+// possibly reading what an LDS DMA in flight writes, and drains every DMA
+// before it; issued this way the DMA is invisible to it.  A caller orders its
+// DMAs itself: the issuing wave waits with s_waitcnt vmcnt, then a
+// work-group barrier, before any wave reads what they wrote.  (The
+// compiler's own vmcnt waits stay correct: DMAs it does not know of only make
+// them wait longer.)  It sets M0, which the compiler treats as reserved and
+// does not track across asm: a kernel that uses it may hold nothing of its
+// own in M0 (the prefill kernel uses M0 for these DMAs only).
+__device__ inline void dma16_asm(rsrc_words_t r, void* dst, int off) {
+  const uint32_t lds = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_ptr_t)dst));
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(lds), "v"(off), "s"(r)
+               : "memory");
+}
+
 // A pointer every lane holds, broadcast from lane 0 so the compiler keeps it
 // (and descriptors built from it) in scalar registers.
 template <typename T>
@@ -329,21 +354,22 @@ struct WaveAttn {
   // masked scores (-inf) give P = 0 and the first visible score moves it.
   // sl = scale * log2(e) > 0 (a negative scale is folded into Q).
 
-  // Raw S^T of a tile: lane (n, g) gets keys 4g+j (sc[s][0]) and 16+4g+j
+  // Raw S^T of a tile in two parts, so that the reads can be issued well
+  // ahead of the products: the K operands (K row 16h + n, logical chunk
+  // 4c + g), then lane (n, g) gets keys 4g+j (sc[s][0]) and 16+4g+j
   // (sc[s][1]) of m-row n.
   template <class Tile>
-  __device__ void qk_lds(const char* kt, f32x4 (&sc)[NM][2]) const {
+  __device__ void k_operands(const char* kt, int h, u32x4 (&kop)[NC]) const {
 #pragma unroll
-    for (int s = 0; s < NM; ++s) sc[s][0] = sc[s][1] = f32x4{0.f, 0.f, 0.f, 0.f};
-    // K row 16h + n, head_dim 8(4c+g) .. 8(4c+g)+7 (logical chunk 4c+g).
+    for (int c = 0; c < NC; ++c) kop[c] = *reinterpret_cast<const u32x4*>(kt + Tile::offset(16 * h + n, 4 * c + g));
+  }
+  __device__ void qk_ops(const u32x4 (&kop)[NC], int h, f32x4 (&sc)[NM][2]) const {
 #pragma unroll
-    for (int h = 0; h < 2; ++h)
+    for (int s = 0; s < NM; ++s) sc[s][h] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int c = 0; c < NC; ++c) {
-        const u32x4 kop = *reinterpret_cast<const u32x4*>(kt + Tile::offset(16 * h + n, 4 * c + g));
+    for (int c = 0; c < NC; ++c)
 #pragma unroll
-        for (int s = 0; s < NM; ++s) sc[s][h] = TT::mfma(kop, qf[s][c], sc[s][h]);
-      }
+      for (int s = 0; s < NM; ++s) sc[s][h] = TT::mfma(kop[c], qf[s][c], sc[s][h]);
   }
 
   // Local (per-lane) max of each m-row's scores, in log2 units, and whether
@@ -411,6 +437,7 @@ struct WaveAttn {
   // 0 .. VB-1 on entry.
   template <class Tile>
   __device__ void pv_lds(const char* vt, u32x4 (&va)[VB], const u32x4 (&pb)[NM]) {
+    // (va is overwritten when EPL > VB.)
 #pragma unroll
     for (int e0 = 0; e0 < EPL; e0 += VB) {
       if (e0 > 0) read_vt<Tile>(vt, e0, va);
@@ -448,41 +475,12 @@ struct WaveAttn {
     if (g == 0) a.ws_lse[slot * a.G + hh] = ltot > 0.f ? m[s] + __log2f(ltot) : -INFINITY;
   }
 
-  // A tile with no masked key whose scores all stay within kLazyRescale of
-  // their references.  Returns false, with the state untouched, otherwise.
-  // The QK and PV products are fenced off (sched_barrier) from the
-  // instructions around them: the compiler otherwise spreads the softmax and
-  // the next steps' LDS reads among the MFMAs, and the tile runs about 7%
-  // slower (measured on the mixed workload's prefill rows; fencing the V^T
-  // reads off as well loses their overlap with the softmax and most of the
-  // gain).
-  template <class Tile>
-  __device__ bool tile_fast(float sl, const char* kt, const char* vt) {
-    f32x4 sc[NM][2];
-    __builtin_amdgcn_sched_barrier(0);
-    qk_lds<Tile>(kt, sc);
-    __builtin_amdgcn_sched_barrier(0);
-    u32x4 va[VB];
-    read_vt<Tile>(vt, 0, va);
-    u32x4 pb[NM];
-    float lsum[NM];
-    if (__builtin_amdgcn_ballot_w64(probs(sl, sc, pb, lsum)) != 0) return false;
-#pragma unroll
-    for (int s = 0; s < NM; ++s) l[s] += lsum[s];
-    __builtin_amdgcn_sched_barrier(0);
-    pv_lds<Tile>(vt, va, pb);
-    __builtin_amdgcn_sched_barrier(0);
-    return true;
-  }
-
-  // A whole tile with every step: keys at or past kstop or past an m-row's
-  // causal limit masked when MASK, references moved and O rescaled when a
-  // score calls for it.
-  template <class Tile, bool MASK>
-  __device__ void tile_general(float sl, const char* kt, const char* vt, int ts, int kstop) {
-    f32x4 sc[NM][2];
-    qk_lds<Tile>(kt, sc);
-    if constexpr (MASK) {
+  // Softmax of a tile's raw scores sc (from qk_ops): keys at or past kstop
+  // or past an m-row's causal limit masked when `mask`, references moved and
+  // O rescaled when a score calls for it, row sums added; P packed as the B
+  // operand of the tile's PV product.
+  __device__ void softmax_tile(float sl, f32x4 (&sc)[NM][2], bool mask, int ts, int kstop, u32x4 (&pb)[NM]) {
+    if (mask) {
 #pragma unroll
       for (int s = 0; s < NM; ++s)
 #pragma unroll
@@ -493,11 +491,8 @@ struct WaveAttn {
             sc[s][h][j] = (tk < kstop && tk <= qpos[s]) ? sc[s][h][j] : -INFINITY;
           }
     }
-    u32x4 va[VB];
-    read_vt<Tile>(vt, 0, va);
     float mloc[NM];
     if (__builtin_amdgcn_ballot_w64(lazy_check(sl, sc, mloc)) != 0) {
-      // Move every row's reference to its exact running max and rescale.
 #pragma unroll
       for (int s = 0; s < NM; ++s) {
         float mx = fmaxf(mloc[s], __shfl_xor(mloc[s], 16, kWave));
@@ -510,12 +505,10 @@ struct WaveAttn {
         for (int e = 0; e < EPL; ++e) o[s][e] *= corr;
       }
     }
-    u32x4 pb[NM];
     float lsum[NM];
     probs(sl, sc, pb, lsum);
 #pragma unroll
     for (int s = 0; s < NM; ++s) l[s] += lsum[s];
-    pv_lds<Tile>(vt, va, pb);
   }
 
   // Row sums over the four lane groups that share an m-row.
@@ -1070,7 +1063,8 @@ attn_merge_kernel(const AttnArgs a) {
 // through a ring of four slots, three tiles ahead of the one being computed,
 // so each K/V byte is read from HBM once per work-group and from LDS once per
 // wave.  A wave skips tiles wholly past its own causal limit.
-constexpr int kPreWaves = 8;  // two per SIMD
+constexpr int kPreWaves = 8;    // two per SIMD
+constexpr int kPreIssuers = 4;  // the leading wave of each SIMD
 constexpr int kPreKeys = 32;
 constexpr int kPreSlots = 4;
 
@@ -1086,9 +1080,9 @@ struct PreTile {
   static constexpr int RB = 2 * D;               // bytes per key row
   static constexpr int BYTES = kPreKeys * RB;    // bytes per K (or V) tile
   static constexpr int CHUNKS = kPreKeys * CPR;  // chunks per tile
-  // Waves that issue the DMA of a tile, and DMA instructions each (K or V).
-  static constexpr int ISSUERS = CHUNKS / 64 < kPreWaves ? CHUNKS / 64 : kPreWaves;
-  static constexpr int NI = CHUNKS / (64 * ISSUERS);
+  // DMA instructions per issuing wave (K or V): kPreIssuers waves issue a tile.
+  static constexpr int NI = CHUNKS / (64 * kPreIssuers);
+  static_assert(CHUNKS % (64 * kPreIssuers) == 0, "a tile splits evenly over the issuing waves");
   // 128-byte rows (D = 64) share a 256-byte bank line in pairs.
   __host__ __device__ static constexpr int swz(int r) { return D == 64 ? (r >> 1) & 7 : r & 15; }
   __host__ __device__ static constexpr int offset(int r, int lc) { return r * RB + 16 * (lc ^ swz(r)); }
@@ -1110,6 +1104,14 @@ __device__ inline void lds_barrier() {
   asm volatile("" ::: "memory");
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
+}
+
+// lds_barrier that also ends an instruction-scheduling region: nothing moves
+// across it, so the half-steps of the prefill loop stay apart.
+__device__ inline void half_barrier() {
+  __builtin_amdgcn_sched_barrier(0);
+  lds_barrier();
+  __builtin_amdgcn_sched_barrier(0);
 }
 
 template <class TT, int D, int NM>
@@ -1203,33 +1205,18 @@ attn_prefill_kernel(const AttnArgs a) {
   const int kend = nq > 0 ? max(causal ? min(klen, off + q0 + nq) : klen, 0) : 0;
   const int qpos_min = causal ? off + q0 : INT_MAX;
 
-  WA wa;
-  wa.setup(a, lane, kvh, qs, q0, nq, off);
-  // Scores in log2 units are S * sl with sl > 0: a negative scale flips the
-  // sign of Q (exact), a zero scale becomes a negligible positive one.
-  float sl = a.scale_log2;
-  if (sl < 0.f) {
-#pragma unroll
-    for (int s = 0; s < NM; ++s)
-#pragma unroll
-      for (int c = 0; c < WA::NC; ++c) wa.qf[s][c] ^= u32x4{0x80008000u, 0x80008000u, 0x80008000u, 0x80008000u};
-    sl = -sl;
-  }
-  sl = fmaxf(sl, 1e-30f);
-#pragma unroll
-  for (int s = 0; s < NM; ++s) wa.m[s] = -FLT_MAX;
-
-  // DMA: issuing wave w, instruction i fills chunks 64 (NI w + i) .. of a
-  // tile; all of a wave's chunks lie in the one 16-key half hw.  Lane L's
-  // chunk is physical chunk pc of row pr; it loads logical chunk
-  // pc ^ swz(pr) of that key.
+  // DMA: issuing wave w (the leading group), instruction i fills chunks
+  // 64 (NI w + i) .. of a tile; all of a wave's chunks lie in the one 16-key
+  // half hw.  Lane L's chunk is physical chunk pc of row pr; it loads logical
+  // chunk pc ^ swz(pr) of that key.
   constexpr int NI = Tile::NI;
-  const bool issuer = wave < Tile::ISSUERS;
-  const int hw = __builtin_amdgcn_readfirstlane((64 * NI * wave) / (16 * Tile::CPR));
+  const int grp = wave / kPreIssuers;  // 0 leads, 1 runs one half-step behind
+  const bool issuer = grp == 0;
+  const int hw = __builtin_amdgcn_readfirstlane(issuer ? (64 * NI * wave) / (16 * Tile::CPR) : 0);
   uint32_t koff[NI], voff[NI];
 #pragma unroll
   for (int i = 0; i < NI; ++i) {
-    const int p = 64 * (NI * wave + i) + lane;
+    const int p = 64 * (NI * (issuer ? wave : 0) + i) + lane;
     const int pr = p / Tile::CPR, pc = p % Tile::CPR;
     const int lc = pc ^ Tile::swz(pr);
     koff[i] = 2u * ((pr & 15) * static_cast<uint32_t>(a.k_st) + 8u * lc);
@@ -1254,13 +1241,12 @@ attn_prefill_kernel(const AttnArgs a) {
       (const __attribute__((address_space(4))) int32_t*)btrow;
   auto bt_at = [&](int blk) -> int { return btc[min(blk, max(nb_row - 1, 0))]; };
   int nblk = (k0 + 16 * hw) / bs, nbo = (k0 + 16 * hw) % bs;
-  int nid = nb_row > 0 ? bt_at(nblk) : 0;
+  int nid = issuer && nb_row > 0 ? bt_at(nblk) : 0;
 
   // DMA of tile t (the next in order) into ring slot S.  The descriptor of
   // the half starts at its first key and covers only keys below kend_g: the
   // rows past it read as zeros.
   auto issue = [&](int S, int t) {
-    if (!issuer) return;
     const uint32_t b = min(static_cast<uint32_t>(max(nid, 0)), nblocks - 1);
     const int rows = min(max(kend_g - (k0 + kPreKeys * t + 16 * hw), 0), 16);
     const char* kb = kbase + (static_cast<uint64_t>(b) * ksb + static_cast<uint32_t>(nbo) * kst);
@@ -1279,80 +1265,122 @@ attn_prefill_kernel(const AttnArgs a) {
     }
     nid = bt_at(nblk);
     char* dst = slot(S) + 1024 * NI * wave;
+    const rsrc_words_t kr = rsrc_words(kb, nrk), vr = rsrc_words(vb, nrv);
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
-      dma16(block_rsrc(kb, nrk), dst + 1024 * i, koff[i]);
-      dma16(block_rsrc(vb, nrv), dst + Tile::BYTES + 1024 * i, voff[i]);
+      dma16_asm(kr, dst + 1024 * i, koff[i]);
+      dma16_asm(vr, dst + Tile::BYTES + 1024 * i, voff[i]);
     }
   };
 
-  // Every wave walks all ntiles tiles in step.  Tile t sits in slot t % 4;
-  // while it is computed, tiles t+1 and t+2 are landing and the DMA of tile
-  // t+3 is issued.  After tile t: wait until tile t+1 has landed (this wave's
-  // DMAs of tiles t+2 and t+3 may stay in flight), then one barrier.
+  // Ping-pong over half-steps.  Tile t is two half-steps: M(t), the MFMA
+  // work -- PV of tile t-1 and QK of tile t -- and X(t), the softmax of tile
+  // t.  Every half-step ends in one work-group barrier.  The second wave of
+  // each SIMD (group 1) runs one half-step behind the first (group 0), so
+  // while one is in its MFMA half-step the other is in its softmax: the
+  // matrix core and the VALU work side by side.  Group 1 passes one extra
+  // barrier first and group 0 one extra at the end, so both pass the same
+  // number.
+  //
+  // Group 0 issues the DMA of tile t+2 at the start of M(t), into the slot of
+  // tile t-2, whose V group 1 read last, in its M(t-1), one half-step before.
+  // Group 0 reads tile t first, in M(t); its issuers wait for tile t's DMA
+  // in X(t-1), before the barrier that precedes M(t), leaving tile t+1's DMA
+  // in flight.  Tile t sits in slot t % 4; the loop body is unrolled four
+  // times so that every LDS access names a fixed slot.
   constexpr int PER_TILE = 2 * NI;  // DMA instructions per issuing wave and tile
   const int ntiles = (kend_g - k0 + kPreKeys - 1) / kPreKeys;
-  auto finish = [&](int t) {
-    if (t + 1 < ntiles) {
-      const int later = min(t + 3, ntiles - 1) - (t + 1);
-      if (later >= 2) wait_vmcnt<2 * PER_TILE>();
-      else if (later == 1) wait_vmcnt<PER_TILE>();
-      else wait_vmcnt<0>();
-    }
-    lds_barrier();
-  };
-  if (ntiles > 0) issue(0, 0);
-  if (ntiles > 1) issue(1, 1);
-  if (ntiles > 2) issue(2, 2);
-  if (ntiles > 2) wait_vmcnt<2 * PER_TILE>();
-  else if (ntiles > 1) wait_vmcnt<PER_TILE>();
-  else wait_vmcnt<0>();
-  lds_barrier();
-
-  // Tiles [0, nfull) have no key masked for this wave.  Runs of four of them
-  // starting at slot 0 go through the fast path, one straight-line loop body
-  // per four tiles (a single path for the accumulators); a fast tile that
-  // would have to move a reference -- always the first -- and every other
-  // tile take the general path one at a time.
+  // Tiles [0, nfull) have no key masked for this wave; tiles from kend on
+  // have no key it sees.
   const int nfull = ((causal ? min(kend, qpos_min + 1) : kend) - k0) / kPreKeys;
-  auto fast = [&](int S, int t) -> bool {
-    if (t + 3 < ntiles) issue((S + 3) % kPreSlots, t + 3);
-    const char* kt = slot(S);
-    return wa.template tile_fast<Tile>(sl, kt, kt + Tile::BYTES);
-  };
-  auto general = [&](int S, int t, bool issued) {
-    if (!issued && t + 3 < ntiles) issue((S + 3) % kPreSlots, t + 3);
-    const char* kt = slot(S);
+  // Prologue: tiles 0 and 1, then Q; one wait for all of it.  (Q's loads are
+  // the only vector loads the compiler knows of: waited for here, none is
+  // pending inside the loop, so it adds no wait there that would also drain
+  // the DMAs.)
+  if (issuer && ntiles > 0) issue(0, 0);
+  if (issuer && ntiles > 1) issue(1, 1);
+  WA wa;
+  wa.setup(a, lane, kvh, qs, q0, nq, off);
+  wait_vmcnt<0>();
+  // Scores in log2 units are S * sl with sl > 0: a negative scale flips the
+  // sign of Q (exact), a zero scale becomes a negligible positive one.
+  float sl = a.scale_log2;
+  if (sl < 0.f) {
+#pragma unroll
+    for (int s = 0; s < NM; ++s)
+#pragma unroll
+      for (int c = 0; c < WA::NC; ++c) wa.qf[s][c] ^= u32x4{0x80008000u, 0x80008000u, 0x80008000u, 0x80008000u};
+    sl = -sl;
+  }
+  sl = fmaxf(sl, 1e-30f);
+#pragma unroll
+  for (int s = 0; s < NM; ++s) wa.m[s] = -FLT_MAX;
+  half_barrier();
+  if (grp == 1) half_barrier();
+
+  // LDS reads never wait inside a half-step: M(t) issues all of tile t's K
+  // reads first and runs PV(t-1) from registers while they land; X(t) reads
+  // tile t's V^T operands (the first VB head_dim blocks) while the softmax
+  // runs, for PV(t) in M(t+1).
+  u32x4 pb[NM];           // P of the previous tile, for its PV
+  u32x4 va[WA::VB];       // its V^T operands
+  bool pv_due = false;    // the previous tile had keys this wave sees
+  auto step = [&](auto S_, int t) {
+    constexpr int S = decltype(S_)::value;
+    // M(t)
+    if (issuer && t + 2 < ntiles) issue((S + 2) & 3, t + 2);
     const int ts = k0 + kPreKeys * t;
-    if (t < nfull)
-      wa.template tile_general<Tile, false>(sl, kt, kt + Tile::BYTES, ts, kend);
-    else if (ts < kend)
-      wa.template tile_general<Tile, true>(sl, kt, kt + Tile::BYTES, ts, kend);
-  };
-  int t = 0;
-  while (t < ntiles) {
-    bool issued = false;
-    if ((t & 3) == 0) {
-      while (t + 3 < nfull) {
-        if (!fast(0, t)) { issued = true; break; }
-        finish(t++);
-        if (!fast(1, t)) { issued = true; break; }
-        finish(t++);
-        if (!fast(2, t)) { issued = true; break; }
-        finish(t++);
-        if (!fast(3, t)) { issued = true; break; }
-        finish(t++);
+    const bool live = t < ntiles && ts < kend;
+    f32x4 sc[NM][2];
+    if constexpr (WA::NC <= 4) {
+      u32x4 kop[2][WA::NC];
+      if (live) {
+        wa.template k_operands<Tile>(slot(S), 0, kop[0]);
+        wa.template k_operands<Tile>(slot(S), 1, kop[1]);
+      }
+      if (pv_due) wa.template pv_lds<Tile>(slot((S + 3) & 3) + Tile::BYTES, va, pb);
+      if (live) {
+        wa.qk_ops(kop[0], 0, sc);
+        wa.qk_ops(kop[1], 1, sc);
+      }
+    } else {
+      // D = 256 (registers): one 16-key half of K operands at a time, and
+      // the V^T operands read here rather than ahead.
+      u32x4 kop[WA::NC];
+      if (live) wa.template k_operands<Tile>(slot(S), 0, kop);
+      if (pv_due) {
+        wa.template read_vt<Tile>(slot((S + 3) & 3) + Tile::BYTES, 0, va);
+        wa.template pv_lds<Tile>(slot((S + 3) & 3) + Tile::BYTES, va, pb);
+      }
+      if (live) {
+        wa.qk_ops(kop, 0, sc);
+        wa.template k_operands<Tile>(slot(S), 1, kop);
+        wa.qk_ops(kop, 1, sc);
       }
     }
-    if (t >= ntiles) break;
-    switch (t & 3) {
-      case 0: general(0, t, issued); break;
-      case 1: general(1, t, issued); break;
-      case 2: general(2, t, issued); break;
-      default: general(3, t, issued); break;
+    half_barrier();
+    // X(t)
+    if (issuer && t + 1 < ntiles) {
+      if (t + 2 < ntiles) wait_vmcnt<PER_TILE>();
+      else wait_vmcnt<0>();
     }
-    finish(t++);
+    if (live) {
+      if constexpr (WA::NC <= 4) wa.template read_vt<Tile>(slot(S) + Tile::BYTES, 0, va);
+      wa.softmax_tile(sl, sc, t >= nfull, ts, kend, pb);
+    }
+    pv_due = live;
+    half_barrier();
+  };
+  for (int t = 0; t <= ntiles; t += 4) {
+    step(std::integral_constant<int, 0>{}, t);
+    if (t + 1 > ntiles) break;
+    step(std::integral_constant<int, 1>{}, t + 1);
+    if (t + 2 > ntiles) break;
+    step(std::integral_constant<int, 2>{}, t + 2);
+    if (t + 3 > ntiles) break;
+    step(std::integral_constant<int, 3>{}, t + 3);
   }
+  if (grp == 0) half_barrier();
   float ltot[NM];
   wa.row_sums(ltot);
 #pragma unroll
