@@ -186,10 +186,10 @@ __device__ inline int decode_visible_keys(const AttnArgs& a, int row) {
 }
 
 // Prefill tiles move their softmax reference only when a score exceeds it by
-// more than this many log2 units (P < 2^kLazyRescale: with up to 2^31 keys and
-// |V| < 2^70 the fp32 sums stay finite).
-constexpr float kLazyRescale = 16.f;
-constexpr float kLazyLimit = 65536.f;  // 2^kLazyRescale
+// more than this many log2 units, so P <= 2^15: finite as an fp16 operand
+// (largest 65504), and with up to 2^31 keys and |V| < 2^70 the fp32 sums stay
+// finite.
+constexpr float kLazyRescale = 15.f;
 
 
 // One wavefront's attention state and key loop.
@@ -201,8 +201,10 @@ struct WaveAttn {
   using st = uint16_t;
 
   int n, g;
-  // m-row s*16 + n of this lane: query index (within the block), head, validity
-  int mq[NM], mh[NM], qpos[NM];
+  // m-row s*16 + n of this lane: causal limit (key positions up to it are visible) and validity
+  int kvh_;                  // the work's kv head (uniform)
+  int qbase_, lg_g_;         // causal limit of query 0 (INT_MAX: none), log2 G (uniform)
+  int qpos[NM];
   bool mval[NM];
   u32x4 qf[NM][NC];  // Q as the B operand of S^T = K . Q^T
   float m[NM], l[NM];
@@ -214,19 +216,21 @@ struct WaveAttn {
                         int off) {
     n = lane & 15;
     g = lane >> 4;
+    kvh_ = kvh;
     const int G = a.G;
+    qbase_ = a.causal ? off + q0 : INT_MAX;
+    lg_g_ = __builtin_ctz(static_cast<unsigned>(G));
 #pragma unroll
     for (int s = 0; s < NM; ++s) {
       const int i = 16 * s + n;
-      mq[s] = i / G;
-      mh[s] = kvh * G + (i % G);
-      mval[s] = mq[s] < nq && qs + q0 + mq[s] < a.total_q;
-      qpos[s] = mval[s] ? (a.causal ? off + q0 + mq[s] : INT_MAX) : -1;
+      const int mq = i / G, mh = kvh * G + (i % G);
+      mval[s] = mq < nq && qs + q0 + mq < a.total_q;
+      qpos[s] = mval[s] ? (a.causal ? off + q0 + mq : INT_MAX) : -1;
 #pragma unroll
       for (int c = 0; c < NC; ++c) qf[s][c] = u32x4{0, 0, 0, 0};
       if (mval[s]) {
-        const st* qp = static_cast<const st*>(a.q) + (qs + q0 + mq[s]) * a.q_st +
-                       static_cast<int64_t>(mh[s]) * a.q_sh;
+        const st* qp = static_cast<const st*>(a.q) + (qs + q0 + mq) * a.q_st +
+                       static_cast<int64_t>(mh) * a.q_sh;
 #pragma unroll
         for (int c = 0; c < NC; ++c)
           qf[s][c] = *reinterpret_cast<const u32x4*>(qp + 8 * (4 * c + g));
@@ -237,6 +241,15 @@ struct WaveAttn {
       for (int e = 0; e < EPL; ++e) o[s][e] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
   }
+
+  // Query (within the block), query head and causal limit of m-row s of
+  // this lane, recomputed where needed rather than held in registers through
+  // the loop (G a power of two).
+  __device__ int qlimit(int s) const {
+    return mval[s] ? (qbase_ == INT_MAX ? INT_MAX : qbase_ + ((16 * s + n) >> lg_g_)) : -1;
+  }
+  __device__ int row_query(const AttnArgs& a, int s) const { return (16 * s + n) / a.G; }
+  __device__ int row_head(const AttnArgs& a, int s) const { return kvh_ * a.G + (16 * s + n) % a.G; }
 
   // Issues the loads of one 16-token slice of kv head kvh: tokens bo..bo+15
   // of physical block id.
@@ -389,8 +402,7 @@ struct WaveAttn {
   // lane's row sums.  Returns whether some P exceeds 2^kLazyRescale (a score
   // more than kLazyRescale above its reference, which the fast path may not
   // take); the test reads P, so P is formed before any branch on it.
-  __device__ bool probs(float sl, const f32x4 (&sc)[NM][2], u32x4 (&pb)[NM], float (&lsum)[NM]) const {
-    bool big = false;
+  __device__ void probs(float sl, const f32x4 (&sc)[NM][2], u32x4 (&pb)[NM]) {
 #pragma unroll
     for (int s = 0; s < NM; ++s) {
       float p[2][4];
@@ -398,14 +410,10 @@ struct WaveAttn {
       for (int h = 0; h < 2; ++h)
 #pragma unroll
         for (int j = 0; j < 4; ++j) p[h][j] = fast_exp2(__builtin_fmaf(sc[s][h][j], sl, -m[s]));
-      lsum[s] = ((p[0][0] + p[0][1]) + (p[0][2] + p[0][3])) + ((p[1][0] + p[1][1]) + (p[1][2] + p[1][3]));
-      const float pm = fmaxf(fmaxf(fmaxf(p[0][0], p[0][1]), fmaxf(p[0][2], p[0][3])),
-                             fmaxf(fmaxf(p[1][0], p[1][1]), fmaxf(p[1][2], p[1][3])));
-      big = big || !(pm <= kLazyLimit);
+      l[s] += ((p[0][0] + p[0][1]) + (p[0][2] + p[0][3])) + ((p[1][0] + p[1][1]) + (p[1][2] + p[1][3]));
       pb[s] = u32x4{TT::pack2(p[0][0], p[0][1]), TT::pack2(p[0][2], p[0][3]),
                     TT::pack2(p[1][0], p[1][1]), TT::pack2(p[1][2], p[1][3])};
     }
-    return big;
   }
 
   // V^T operands of a tile, read with ds_read_b64_tr_b16.  Within a 16-lane
@@ -452,13 +460,13 @@ struct WaveAttn {
   // layout of pv_lds, to token t.
   __device__ void store_final_blocks(const AttnArgs& a, int s, int64_t t, float ltot) const {
     const float inv = ltot > 0.f ? 1.f / ltot : 0.f;
-    st* op = static_cast<st*>(a.o) + t * a.o_st + static_cast<int64_t>(mh[s]) * a.o_sh + 4 * g;
+    st* op = static_cast<st*>(a.o) + t * a.o_st + static_cast<int64_t>(row_head(a, s)) * a.o_sh + 4 * g;
 #pragma unroll
     for (int e = 0; e < EPL; ++e)
       *reinterpret_cast<u32x2*>(op + 16 * e) =
           u32x2{TT::pack2(o[s][e][0] * inv, o[s][e][1] * inv), TT::pack2(o[s][e][2] * inv, o[s][e][3] * inv)};
     if (a.lse && g == 0)
-      a.lse[t * a.l_st + static_cast<int64_t>(mh[s]) * a.l_sh] =
+      a.lse[t * a.l_st + static_cast<int64_t>(row_head(a, s)) * a.l_sh] =
           ltot > 0.f ? (m[s] + __log2f(ltot)) * kLn2 : -INFINITY;
   }
 
@@ -477,8 +485,8 @@ struct WaveAttn {
 
   // Softmax of a tile's raw scores sc (from qk_ops): keys at or past kstop
   // or past an m-row's causal limit masked when `mask`, references moved and
-  // O rescaled when a score calls for it, row sums added; P packed as the B
-  // operand of the tile's PV product.
+  // O and the row sums rescaled when a score calls for it, row sums added;
+  // P packed as the B operand of the tile's PV product.
   __device__ void softmax_tile(float sl, f32x4 (&sc)[NM][2], bool mask, int ts, int kstop, u32x4 (&pb)[NM]) {
     if (mask) {
 #pragma unroll
@@ -488,7 +496,7 @@ struct WaveAttn {
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
             const int tk = ts + 16 * h + 4 * g + j;
-            sc[s][h][j] = (tk < kstop && tk <= qpos[s]) ? sc[s][h][j] : -INFINITY;
+            sc[s][h][j] = (tk < kstop && tk <= qlimit(s)) ? sc[s][h][j] : -INFINITY;
           }
     }
     float mloc[NM];
@@ -505,10 +513,7 @@ struct WaveAttn {
         for (int e = 0; e < EPL; ++e) o[s][e] *= corr;
       }
     }
-    float lsum[NM];
-    probs(sl, sc, pb, lsum);
-#pragma unroll
-    for (int s = 0; s < NM; ++s) l[s] += lsum[s];
+    probs(sl, sc, pb);
   }
 
   // Row sums over the four lane groups that share an m-row.
@@ -518,31 +523,6 @@ struct WaveAttn {
       const float t = l[s] + __shfl_xor(l[s], 16, kWave);
       ltot[s] = t + __shfl_xor(t, 32, kWave);
     }
-  }
-
-  // Final O (q dtype) and natural-log LSE of m-row s, to token t.
-  __device__ void store_final(const AttnArgs& a, int s, int64_t t, float ltot) const {
-    const float inv = ltot > 0.f ? 1.f / ltot : 0.f;
-    st* op = static_cast<st*>(a.o) + t * a.o_st + static_cast<int64_t>(mh[s]) * a.o_sh;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      uint32_t w[VW];
-#pragma unroll
-      for (int e2 = 0; e2 < VW; ++e2)
-        w[e2] = TT::pack2(o[s][2 * e2][j] * inv, o[s][2 * e2 + 1][j] * inv);
-      st* dp = op + EPL * (4 * g + j);
-      if constexpr (VW == 2) {
-        *reinterpret_cast<u32x2*>(dp) = u32x2{w[0], w[1]};
-      } else {
-#pragma unroll
-        for (int c = 0; c < VW / 4; ++c)
-          *reinterpret_cast<u32x4*>(dp + 8 * c) =
-              u32x4{w[4 * c], w[4 * c + 1], w[4 * c + 2], w[4 * c + 3]};
-      }
-    }
-    if (a.lse && g == 0)
-      a.lse[t * a.l_st + static_cast<int64_t>(mh[s]) * a.l_sh] =
-          ltot > 0.f ? (m[s] + __log2f(ltot)) * kLn2 : -INFINITY;
   }
 };
 
@@ -1282,23 +1262,27 @@ attn_prefill_kernel(const AttnArgs a) {
   // barrier first and group 0 one extra at the end, so both pass the same
   // number.
   //
-  // Group 0 issues the DMA of tile t+2 at the start of M(t), into the slot of
-  // tile t-2, whose V group 1 read last, in its M(t-1), one half-step before.
-  // Group 0 reads tile t first, in M(t); its issuers wait for tile t's DMA
-  // in X(t-1), before the barrier that precedes M(t), leaving tile t+1's DMA
-  // in flight.  Tile t sits in slot t % 4; the loop body is unrolled four
-  // times so that every LDS access names a fixed slot.
+  // The DMA is group 0's scalar and issue work, kept out of its MFMA
+  // half-steps: in X(t), group 0 waits for its part of tile t+1 (read first
+  // in M(t+1), after the barrier that ends X(t)), then issues tile t+LEAD
+  // into the slot of tile t+LEAD-4, whose last reads are done: at LEAD 3 (V^T
+  // read in X), tile t-1's V^T in group 1's X(t-1), one half-step before;
+  // at LEAD 2 (D = 256 reads V^T in M), tile t-2's in group 1's M(t-1).  Tile
+  // t sits in slot t % 4; the loop body is unrolled four times so that every
+  // LDS access names a fixed slot.
   constexpr int PER_TILE = 2 * NI;  // DMA instructions per issuing wave and tile
+  constexpr int LEAD = WA::NC <= 4 ? 3 : 2;
   const int ntiles = (kend_g - k0 + kPreKeys - 1) / kPreKeys;
   // Tiles [0, nfull) have no key masked for this wave; tiles from kend on
   // have no key it sees.
   const int nfull = ((causal ? min(kend, qpos_min + 1) : kend) - k0) / kPreKeys;
-  // Prologue: tiles 0 and 1, then Q; one wait for all of it.  (Q's loads are
-  // the only vector loads the compiler knows of: waited for here, none is
-  // pending inside the loop, so it adds no wait there that would also drain
-  // the DMAs.)
+  // Prologue: tiles 0 .. LEAD-1, then Q; one wait for all of it.  (Q's loads
+  // are the only vector loads the compiler knows of: waited for here, none
+  // is pending inside the loop, so it adds no wait there that would also
+  // drain the DMAs.)
   if (issuer && ntiles > 0) issue(0, 0);
   if (issuer && ntiles > 1) issue(1, 1);
+  if (LEAD > 2 && issuer && ntiles > 2) issue(2, 2);
   WA wa;
   wa.setup(a, lane, kvh, qs, q0, nq, off);
   wait_vmcnt<0>();
@@ -1320,19 +1304,20 @@ attn_prefill_kernel(const AttnArgs a) {
 
   // LDS reads never wait inside a half-step: M(t) issues all of tile t's K
   // reads first and runs PV(t-1) from registers while they land; X(t) reads
-  // tile t's V^T operands (the first VB head_dim blocks) while the softmax
-  // runs, for PV(t) in M(t+1).
+  // tile t's V^T operands while the softmax runs, for PV(t) in M(t+1).  D =
+  // 256 (registers): K half a tile at a time, and tile t-1's V^T read in
+  // M(t) itself.
+  constexpr bool kVAhead = WA::NC <= 4;
   u32x4 pb[NM];           // P of the previous tile, for its PV
   u32x4 va[WA::VB];       // its V^T operands
   bool pv_due = false;    // the previous tile had keys this wave sees
   auto step = [&](auto S_, int t) {
     constexpr int S = decltype(S_)::value;
     // M(t)
-    if (issuer && t + 2 < ntiles) issue((S + 2) & 3, t + 2);
     const int ts = k0 + kPreKeys * t;
     const bool live = t < ntiles && ts < kend;
     f32x4 sc[NM][2];
-    if constexpr (WA::NC <= 4) {
+    if constexpr (kVAhead) {
       u32x4 kop[2][WA::NC];
       if (live) {
         wa.template k_operands<Tile>(slot(S), 0, kop[0]);
@@ -1344,28 +1329,28 @@ attn_prefill_kernel(const AttnArgs a) {
         wa.qk_ops(kop[1], 1, sc);
       }
     } else {
-      // D = 256 (registers): one 16-key half of K operands at a time, and
-      // the V^T operands read here rather than ahead.
-      u32x4 kop[WA::NC];
-      if (live) wa.template k_operands<Tile>(slot(S), 0, kop);
+      u32x4 kh[WA::NC];
+      if (live) wa.template k_operands<Tile>(slot(S), 0, kh);
       if (pv_due) {
         wa.template read_vt<Tile>(slot((S + 3) & 3) + Tile::BYTES, 0, va);
         wa.template pv_lds<Tile>(slot((S + 3) & 3) + Tile::BYTES, va, pb);
       }
       if (live) {
-        wa.qk_ops(kop, 0, sc);
-        wa.template k_operands<Tile>(slot(S), 1, kop);
-        wa.qk_ops(kop, 1, sc);
+        wa.qk_ops(kh, 0, sc);
+        wa.template k_operands<Tile>(slot(S), 1, kh);
+        wa.qk_ops(kh, 1, sc);
       }
     }
     half_barrier();
-    // X(t)
+    // X(t): tiles t+1 .. t+LEAD-1 are in flight; tile t+1 lands before the
+    // barrier that precedes M(t+1).
     if (issuer && t + 1 < ntiles) {
-      if (t + 2 < ntiles) wait_vmcnt<PER_TILE>();
+      if (LEAD > 2 && t + 2 < ntiles) wait_vmcnt<PER_TILE>();
       else wait_vmcnt<0>();
     }
+    if (issuer && t + LEAD < ntiles) issue((S + LEAD) & 3, t + LEAD);
     if (live) {
-      if constexpr (WA::NC <= 4) wa.template read_vt<Tile>(slot(S) + Tile::BYTES, 0, va);
+      if constexpr (kVAhead) wa.template read_vt<Tile>(slot(S) + Tile::BYTES, 0, va);
       wa.softmax_tile(sl, sc, t >= nfull, ts, kend, pb);
     }
     pv_due = live;
@@ -1387,10 +1372,10 @@ attn_prefill_kernel(const AttnArgs a) {
   for (int s = 0; s < NM; ++s) {
     if (!wa.mval[s]) continue;
     if (prefix)
-      wa.store_partial_blocks(a, s, static_cast<int64_t>(pbase) + static_cast<int64_t>(q0 + wa.mq[s]) * pstride,
-                              wa.mh[s] - kvh * a.G, ltot[s]);
+      wa.store_partial_blocks(a, s, static_cast<int64_t>(pbase) + static_cast<int64_t>(q0 + wa.row_query(a, s)) * pstride,
+                              wa.row_head(a, s) - kvh * a.G, ltot[s]);
     else
-      wa.store_final_blocks(a, s, qs + q0 + wa.mq[s], ltot[s]);
+      wa.store_final_blocks(a, s, qs + q0 + wa.row_query(a, s), ltot[s]);
   }
 }
 
