@@ -2380,7 +2380,7 @@ extern "C" int kvhot_paged_attention_noalloc(
   clear_error();
   int64_t need = 0;
   if (schedule) {
-    need = num_merge_units > 0 ? schedule_workspace_bytes : 0;
+    need = num_merge_units > 0 || num_prefix_units > 0 ? schedule_workspace_bytes : 0;
   } else {
     need = kvhot_paged_attention_workspace_bytes(num_rows, total_query, max_q_len, max_k_len, num_q_heads,
                                                  num_kv_heads, head_dim, block_size, partition_tokens, dtype);

@@ -141,6 +141,9 @@ def test_noalloc_rejects_calls_beyond_its_scratch(lib):
     sched = list(args)
     sched[29:35] = [f, 16, 0, 1, 0, (32 << 20) + 1]
     assert lib.kvhot_paged_attention_noalloc(*sched) == -3
+    # shared-prefix units alone (no merge units) need their partials too
+    sched[29:35] = [f, 16, 2, 0, 2, (32 << 20) + 1]
+    assert lib.kvhot_paged_attention_noalloc(*sched) == -3
     # invalid sizes are reported as such
     bad = list(args)
     bad[20] = 30

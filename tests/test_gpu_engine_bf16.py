@@ -14,6 +14,10 @@ request's whole token sequence.
   the step's tokens).
 * Decode-only steps run as replays of DecodeStepGraph after an eager
   prefill.
+* A prefilled request forked five times: six decode rows share their
+  leading blocks (copy-on-write of the last one), so the launch list
+  attends the shared prefix once (shared-prefix units), eagerly and in
+  graph replays.
 
 Every sampled token's logits row is checked against the reference within
 atol 2e-2 / rtol 1e-2, the bf16 bar of the attention parity tests (measured
@@ -148,6 +152,58 @@ def test_bf16_graph_decode_matches_dense_attention(cuda, sea):
             logits_of.setdefault(r.request_id, []).append(graph.logits[i].float().clone())
         sched.update_after_step(out)
     assert replays >= new_tokens - 2
+    for r in reqs:
+        assert len(r.output_token_ids) == new_tokens
+    _check_against_dense(dense, reqs, logits_of)
+
+
+def test_bf16_shared_prefix_decode_matches_dense_attention(cuda, sea):
+    print("[gpu-case] bf16 decode of six rows sharing 18 blocks (a request and five forks), eager then graph",
+          flush=True)
+    model, dense = _models(sea, cuda)
+    nblocks, new_tokens = 48, 7
+    kv = sea.allocate_kv_cache(2, nblocks, 2, 64, dtype=torch.bfloat16, device=cuda)
+    cache = sea._PagedKVCache(kv)
+    bm = sea.BlockManager(nblocks)
+    sched = sea.Scheduler(bm, max_num_batched_tokens=512, min_chunk_size=8)
+    gen = torch.Generator().manual_seed(33)
+    base = sea.Request("p", torch.randint(0, 500, (300,), generator=gen).tolist(), max_new_tokens=new_tokens)
+    sched.add_request(base)
+    logits_of = {}
+    while base.phase != sea.RequestPhase.NEEDS_DECODE:
+        out, logits = sea.sample_step(model, sched, cache, cuda)
+        if base.request_id in out.prefill_final_chunk:
+            logits_of["p"] = [logits[0].float()]
+    reqs = [base]
+    for i in range(5):
+        f = sea.Request(f"f{i}", list(base.prompt_token_ids), max_new_tokens=new_tokens,
+                        output_token_ids=list(base.output_token_ids))
+        f.num_computed_tokens = base.num_computed_tokens
+        f.phase, f.status = base.phase, sea.RequestStatus.RUNNING
+        bm.fork(base, f)
+        sched.running.append(f)
+        logits_of[f.request_id] = list(logits_of["p"])
+        reqs.append(f)
+    # one eager decode step: the shared partial last block is copied on write
+    out, logits = sea.sample_step(model, sched, cache, cuda)
+    assert len(out.blocks_to_copy) >= 5
+    for i, r in enumerate(out.scheduled_requests):
+        logits_of[r.request_id].append(logits[i].float())
+    max_blocks = (300 + new_tokens) // 16 + 1
+    graph = sea.DecodeStepGraph(model, cache, len(reqs), max_blocks, 8, 2, 64, cuda)
+    while sched.has_unfinished_requests():
+        out = sched.schedule()
+        rows = out.scheduled_requests
+        assert len(rows) == len(reqs) and not out.prefill_chunk_sizes
+        if out.blocks_to_copy:
+            cache.copy_blocks([s for s, _ in out.blocks_to_copy], [d for _, d in out.blocks_to_copy])
+        graph.tokens.copy_(torch.tensor([r.output_token_ids[-1] for r in rows], device=cuda))
+        toks = graph.step([r.total_len for r in rows], [list(r.block_table) for r in rows]).cpu().tolist()
+        assert graph._recorded[4] > 0, "the launch list has no shared-prefix units"
+        for i, r in enumerate(rows):
+            r.output_token_ids.append(int(toks[i]))
+            logits_of.setdefault(r.request_id, []).append(graph.logits[i].float().clone())
+        sched.update_after_step(out)
     for r in reqs:
         assert len(r.output_token_ids) == new_tokens
     _check_against_dense(dense, reqs, logits_of)

@@ -59,7 +59,7 @@ def attention(sea, lib, w, T, meta, pt, scheduled, noalloc):
         plan = pak._schedule(meta, device, hq, hkv, d, 16, pt, True, dtype)
         assert plan is not None
         sched, n_dec, n_pre, n_mrg, need, n_pfx = plan
-        assert n_pre > 0 and n_mrg > 0  # prefill beside decode, and partials to merge
+        assert n_pre > 0 and (n_mrg > 0 or n_pfx > 0)  # prefill beside decode, and partials to fold
     else:
         sched, n_dec, n_pre, n_mrg, n_pfx = None, 0, 0, 0, 0
         need = lib.kvhot_paged_attention_workspace_bytes(rows, total, max_q, max_k, hq, hkv, d, 16, pt, dtype)
@@ -94,6 +94,39 @@ def test_noalloc_matches_the_allocating_entry(cuda, sea, scheduled):
         meta = wl.metadata_tensors(w, cuda)
         ref_o, ref_l, need = attention(sea, lib, w, T, meta, 256, scheduled, noalloc=False)
         o, l, need2 = attention(sea, lib, w, T, meta, 256, scheduled, noalloc=True)
+        assert need2 == need <= sea_module("_lib").NOALLOC_SCRATCH_BYTES
+        assert torch.isfinite(o.float()).all() and torch.isfinite(l).all()
+        np.testing.assert_allclose(o.float().cpu().numpy(), ref_o.float().cpu().numpy(), atol=2e-2, rtol=1e-2)
+        np.testing.assert_allclose(l.cpu().numpy(), ref_l.cpu().numpy(), atol=2e-3, rtol=1e-4)
+
+
+def shared(wl, nrows, ctx0, share_blocks, seed):
+    """A prefill chunk and `nrows` decode rows (contexts ctx0, ctx0 + 37, ...)
+    whose block tables start with the same `share_blocks` blocks."""
+    spec = [(9, 60, 51)] + [(1, ctx0 + 37 * i, ctx0 + 37 * i - 1) for i in range(nrows)]
+    w = custom(wl, spec, seed=seed)
+    common = w.rows[1].block_table[:share_blocks].copy()
+    for x in w.rows[1:]:
+        x.block_table = np.concatenate([common, x.block_table[share_blocks:]])
+    return w
+
+
+def test_noalloc_shared_prefix_matches_the_allocating_entry(cuda, sea):
+    """Shared-prefix units (their partials folded into the decode rows) in the
+    scratch array: a batch, then a smaller one."""
+    wl = sea_module("workloads")
+    lib = sea_module("_lib").load()
+    pak = sea_module("paged_attention_kernel")
+    for name, (nrows, ctx0, nb) in (("20 rows sharing 40 blocks", (20, 700, 40)),
+                                    ("5 rows sharing 17 blocks", (5, 300, 17))):
+        announce(f"noalloc vs paged_attention, shared prefix: {name}")
+        w = shared(wl, nrows, ctx0, nb, seed=nrows)
+        T = wl.make_tensors(w, cuda)
+        meta = wl.metadata_tensors(w, cuda)
+        ref_o, ref_l, need = attention(sea, lib, w, T, meta, 0, True, noalloc=False)
+        plan = pak._schedule(meta, cuda, 32, 8, 128, 16, 0, True, sea_module("_lib").dtype_code(torch.bfloat16))
+        assert plan[5] > 0  # shared-prefix units ran
+        o, l, need2 = attention(sea, lib, w, T, meta, 0, True, noalloc=True)
         assert need2 == need <= sea_module("_lib").NOALLOC_SCRATCH_BYTES
         assert torch.isfinite(o.float()).all() and torch.isfinite(l).all()
         np.testing.assert_allclose(o.float().cpu().numpy(), ref_o.float().cpu().numpy(), atol=2e-2, rtol=1e-2)
