@@ -99,6 +99,8 @@ def parse():
 def launch_list_desc(meta, w):
     """The launches of one attention call, from the unit counts of its launch
     list (kvhot_paged_attention_schedule)."""
+    import torch
+
     plans = [p for p in meta.get("_schedules", {}).values() if p is not None]
     if not plans:
         return "one attention call on the padded grid (no launch list)"
