@@ -135,16 +135,27 @@ __device__ inline __amdgpu_buffer_rsrc_t block_rsrc(const void* base, int bytes)
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, 0x00020000);
 }
 
+// Cache policy of the decode kernel's K/V loads: non-temporal (the nt bit).
+// Each K/V byte of a decode launch is read by one wave (a slice serves every
+// query head of its kv head), and rows whose tables share a long prefix have
+// it attended once by prefix units, so the loads leave no reuse to keep.
+// (Rows that share blocks outside a prefix unit, e.g. a few forks, each read
+// them from HBM.)
+#ifndef KVHOT_KV_LOAD_POLICY
+#define KVHOT_KV_LOAD_POLICY 2
+#endif
+constexpr int kKvLoadPolicy = KVHOT_KV_LOAD_POLICY;
+
 // Loads N dwords (N in {2, 4, 8}) at byte offset off (+ uniform soff) of r.
 template <int N>
 __device__ inline void buffer_dwords(__amdgpu_buffer_rsrc_t r, int off, int soff, uint32_t* out) {
   if constexpr (N == 2) {
-    const u32x2 v = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(r, off, soff, 0));
+    const u32x2 v = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(r, off, soff, kKvLoadPolicy));
     out[0] = v.x; out[1] = v.y;
   } else {
 #pragma unroll
     for (int c = 0; c < N / 4; ++c) {
-      const u32x4 v = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off + 16 * c, soff, 0));
+      const u32x4 v = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off + 16 * c, soff, kKvLoadPolicy));
       out[4 * c + 0] = v.x; out[4 * c + 1] = v.y;
       out[4 * c + 2] = v.z; out[4 * c + 3] = v.w;
     }
@@ -265,7 +276,7 @@ struct WaveAttn {
     const int vs = 2 * bo * static_cast<int>(a.v_st);
 #pragma unroll
     for (int c = 0; c < NC; ++c)
-      T.k[c] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(kr, k_lane + 64 * c, ks, 0));
+      T.k[c] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(kr, k_lane + 64 * c, ks, kKvLoadPolicy));
 #pragma unroll
     for (int j = 0; j < 4; ++j)
       buffer_dwords<VW>(vr, 2 * ((4 * g + j) * static_cast<int>(a.v_st) + EPL * n), vs, T.v[j]);
@@ -280,7 +291,7 @@ struct WaveAttn {
     const int vs = 2 * bo * static_cast<int>(a.v_st);
 #pragma unroll
     for (int c = 0; c < NC; ++c)
-      T.k[c] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(kr, k_lane + 64 * c, ks, 0));
+      T.k[c] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(kr, k_lane + 64 * c, ks, kKvLoadPolicy));
 #pragma unroll
     for (int j = 0; j < 4; ++j)
       buffer_dwords<VW>(vr, 2 * ((4 * g + j) * static_cast<int>(a.v_st) + EPL * n), vs, T.v[j]);
@@ -1478,11 +1489,15 @@ attn_generic_kernel(const AttnArgs a) {
 constexpr int64_t kMaxLdsBytes = 64 * 1024;
 constexpr int64_t kCuLdsBytes = 160 * 1024;
 #ifndef KVHOT_MAX_DECODE_WAVES
-#define KVHOT_MAX_DECODE_WAVES 16
+#define KVHOT_MAX_DECODE_WAVES 8
 #endif
 
-// Waves per decode work-group: 16 (head_dim <= 128, whose registers allow 4
-// waves per SIMD) when one slot per wave fits in 64 KiB of LDS, else 8.
+// Waves per decode work-group: 8 (KVHOT_MAX_DECODE_WAVES=16 builds a 16-wave
+// variant for head_dim <= 128 when one slot per wave fits in 64 KiB of LDS).
+// At head_dim 128 the 8-wave kernel takes 145 VGPRs, so a CU holds one such
+// work-group: with non-temporal K/V loads, 8 waves per CU streamed faster
+// than 16 (measured on MI355X, one box, 64-row GQA workload: 52.2 against
+// 54.1 us per call; 55.7 us with 16 waves and cached loads).
 static int decode_waves(int64_t G, int64_t D) {
   if (KVHOT_MAX_DECODE_WAVES >= 16 && D <= 128 && decode_lds_words(16, 16, G, D) * 4 <= kMaxLdsBytes)
     return 16;
@@ -1548,7 +1563,7 @@ static Plan make_plan(int64_t rows, int64_t max_q, int64_t max_k, int64_t Hq,
 constexpr int prefill_nm(int64_t D) { return D == 64 ? 4 : (D == 128 ? 2 : 1); }
 
 // Decode work-groups the current device holds at once, times their waves
-// (4096 when no device can be queried).
+// (one work-group on each of 256 CUs when no device can be queried).
 template <class TT, int D, int W>
 static int decode_groups_per_cu(int64_t G) {
   int n = 0;
@@ -1564,10 +1579,14 @@ static int decode_groups_per_cu(int64_t G) {
 
 template <class TT>
 static int decode_groups_per_cu(int64_t D, int W, int64_t G) {
+#if KVHOT_MAX_DECODE_WAVES >= 16
   if (W == 16) {
     if (D == 64) return decode_groups_per_cu<TT, 64, 16>(G);
     return decode_groups_per_cu<TT, 128, 16>(G);
   }
+#else
+  (void)W;
+#endif
   if (D == 64) return decode_groups_per_cu<TT, 64, 8>(G);
   if (D == 128) return decode_groups_per_cu<TT, 128, 8>(G);
   return decode_groups_per_cu<TT, 256, 8>(G);
@@ -1582,7 +1601,7 @@ static int64_t resident_decode_waves(int dtype, int64_t D, int W, int64_t G) {
                               : decode_groups_per_cu<F16>(D, W, G);
   if (cus <= 0 || per <= 0) {
     (void)hipGetLastError();
-    return 4096;
+    return 256 * static_cast<int64_t>(W);
   }
   return static_cast<int64_t>(cus) * per * W;
 }
@@ -2061,14 +2080,16 @@ static void launch_mfma(const AttnArgs& a, int waves, int64_t rows, int64_t max_
     hipLaunchKernelGGL((attn_prefill_kernel<TT, D, NM>), grid, dim3(64 * kPreWaves), 0, pre_stream, pa);
   }
   if (dec) {
+    bool launched = false;
+#if KVHOT_MAX_DECODE_WAVES >= 16
     if constexpr (D <= 128) {
-      if (waves == 16)
+      if (waves == 16) {
         launch_decode<TT, D, 16>(a, rows, n_dec, stream);
-      else
-        launch_decode<TT, D, 8>(a, rows, n_dec, stream);
-    } else {
-      launch_decode<TT, D, 8>(a, rows, n_dec, stream);
+        launched = true;
+      }
     }
+#endif
+    if (!launched) launch_decode<TT, D, 8>(a, rows, n_dec, stream);
   }
   if (a.sched ? n_merge > 0 : dec && a.max_parts > 1) {
     dim3 mgrid = a.sched ? dim3(static_cast<uint32_t>(n_merge))

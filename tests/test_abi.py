@@ -104,7 +104,7 @@ def test_attention_checks_the_schedule_workspace(lib):
     q3, c4, l2 = _i64(4096, 128, 1), _i64(16384, 1024, 128, 1), _i64(32, 1)
     f = FAKE
     need = 10 * 4 * (128 + 1) * 4  # 10 partials of 4 query heads x (128 + 1) floats
-    # one 16-wave decode work-group and one merge unit
+    # two 8-wave decode work-groups and one merge unit
     args = [f, q3, f, c4, f, c4, f, q3, f, l2, f, 8, f, f, f, f,
             4, 4, 1, 100, 32, 8, 128, 16, 64, 0.1, 1, 2, 0, f, 16, 0, 1, 0, need, f, need - 1, None]
     assert lib.kvhot_paged_attention(*args) == -3
@@ -160,6 +160,12 @@ def test_workspace_bytes(lib):
     # fp32 runs the VALU kernel, which never splits
     assert lib.kvhot_paged_attention_workspace_bytes(64, 64, 1, 2048, 32, 8, 128, 16, 256, 0) == 0
     assert lib.kvhot_paged_attention_workspace_bytes(64, 64, 1, 2048, 30, 8, 128, 16, 256, 2) < 0
+
+
+# Waves per decode work-group, and decode work-groups of a device-full where
+# no device is visible (one on each of 256 CUs).
+W = 8
+GROUPS = 256
 
 
 def _schedule(lib, q_lens, k_lens, offs, hq=32, hkv=8, d=128, pt=0, causal=1, dtype=2, bt=None,
@@ -265,7 +271,7 @@ def test_schedule_lists_every_unit_once(lib):
     # rows: decode 300 keys, decode 40 keys, prefill 20 queries on 50 keys, empty chunk, decode 2000 keys
     q_lens, k_lens, offs = [1, 1, 20, 0, 1], [300, 40, 50, 16, 2000], [299, 39, 30, 16, 1999]
     dec, pre, merge, ws, qs = _schedule(lib, q_lens, k_lens, offs, pt=1024)
-    _check_decode_schedule(dec, merge, ws, qs, 16, {0: 300, 1: 40, 4: 2000}, 8, pt=1024)
+    _check_decode_schedule(dec, merge, ws, qs, W, {0: 300, 1: 40, 4: 2000}, 8, pt=1024)
     # the 2000-key row has two 1024-key partitions per kv head, the others one
     assert sorted(merge[:, 2].tolist()) == [2] * 8
     # prefill: 20 queries, 64 per work-group (4 waves x 64 m-rows / G=4) -> 1 block x 8 kv heads;
@@ -292,7 +298,7 @@ def test_schedule_prefill_blocks_longest_first(lib):
 def test_schedule_uncut_when_balanced(lib):
     """Many rows of mixed lengths (the 64-row GQA decode shape): whole
     (row, kv head) segments packed longest first fit one device-full (256
-    work-groups of 16 waves when no device is queried) within a merge
+    work-groups of 8 waves when no device is queried) within a merge
     launch's worth of slices of the even cut, so no segment is cut and there
     is no merge launch."""
     import numpy as np
@@ -301,7 +307,7 @@ def test_schedule_uncut_when_balanced(lib):
     ctx = rng.integers(128, 2048, size=64, endpoint=True)
     dec, pre, merge, ws, qs = _schedule(lib, [1] * 64, ctx, ctx - 1)
     assert len(pre) == 0
-    loads = _check_decode_schedule(dec, merge, ws, qs, 16, dict(enumerate(ctx.tolist())), 8)
+    loads = _check_decode_schedule(dec, merge, ws, qs, W, dict(enumerate(ctx.tolist())), 8)
     total = sum(-(-int(c) // 16) for c in ctx) * 8
     target = -(-total // 256)
     assert len(merge) == 0 and ws == 0
@@ -322,11 +328,11 @@ def test_schedule_uncut_mixes_kv_heads(lib):
     for lo, hi, rows, want in ((1000, 1100, 256, 8), (128, 2048, 64, 2)):
         ctx = rng.integers(lo, hi, size=rows, endpoint=True)
         dec, pre, merge, ws, qs = _schedule(lib, [1] * rows, ctx, ctx - 1)
-        loads = _check_decode_schedule(dec, merge, ws, qs, 16, dict(enumerate(ctx.tolist())), 8)
+        loads = _check_decode_schedule(dec, merge, ws, qs, W, dict(enumerate(ctx.tolist())), 8)
         assert len(merge) == 0
         total = sum(-(-int(c) // 16) for c in ctx) * 8
         assert max(loads) <= -(-total // 256) + 13
-        heads = [len({w["kvh"] for w in dec[g:g + 16] if w}) for g in range(0, len(dec), 16)]
+        heads = [len({w["kvh"] for w in dec[g:g + W] if w}) for g in range(0, len(dec), W)]
         assert min(heads) >= want, (rows, sorted(set(heads)))
 
 
@@ -336,7 +342,7 @@ def test_schedule_cuts_long_rows(lib):
     leaves at least 4 slices on either side."""
     ctx = [32768] * 4 + [1000, 3000]
     dec, pre, merge, ws, qs = _schedule(lib, [1] * len(ctx), ctx, [c - 1 for c in ctx])
-    loads = _check_decode_schedule(dec, merge, ws, qs, 16, dict(enumerate(ctx)), 8)
+    loads = _check_decode_schedule(dec, merge, ws, qs, W, dict(enumerate(ctx)), 8)
     total = sum(-(-c // 16) for c in ctx) * 8
     target = -(-total // 256)
     assert len(merge) > 0 and ws > 0
@@ -346,12 +352,12 @@ def test_schedule_cuts_long_rows(lib):
 
 def test_schedule_tiny_rows_and_empty_rows(lib):
     """Rows with no visible key still get a wave (it writes zeros); many tiny
-    rows are packed at most 16 ranges per work-group, unsplit."""
+    rows are packed at most 8 ranges per work-group, unsplit."""
     q_lens = [1] * 40
     k_lens = [0, 5] + [17] * 38
     offs = [0, 4] + [16] * 38
     dec, pre, merge, ws, qs = _schedule(lib, q_lens, k_lens, offs, hq=8, hkv=8, d=64)
-    _check_decode_schedule(dec, merge, ws, qs, 16, dict(enumerate(min(k, o + 1) for k, o in zip(k_lens, offs))),
+    _check_decode_schedule(dec, merge, ws, qs, W, dict(enumerate(min(k, o + 1) for k, o in zip(k_lens, offs))),
                            8, G=1, D=64)
     assert len(merge) == 0 and ws == 0
 
@@ -417,8 +423,8 @@ def test_schedule_shared_prefix_units(lib):
     assert ws == nparts_total * pb
     # decode segments of every (row, kv head)
     segs = {}
-    for g0 in range(0, len(dec), 16):
-        for wv in dec[g0:g0 + 16]:
+    for g0 in range(0, len(dec), W):
+        for wv in dec[g0:g0 + W]:
             if wv is not None:
                 segs.setdefault((wv["row"], wv["kvh"]), []).append((g0, wv))
     pidx_of = {}
@@ -494,7 +500,7 @@ def test_schedule_shared_prefix_needs_enough_keys(lib):
 def test_schedule_shared_prefix_stays_within_one_device_fill(lib):
     """256 rows sharing 64 blocks with private tails of 64..512 keys (the
     prefix-sharing workload's shape): the tails, which are never cut, are
-    packed into at most one device-full of decode work-groups (256 of 16
+    packed into at most one device-full of decode work-groups (256 of 8
     waves where no device is visible) with balanced loads."""
     import numpy as np
 
@@ -506,8 +512,8 @@ def test_schedule_shared_prefix_stays_within_one_device_fill(lib):
     bt[:, :64] = 7 + np.arange(64)
     dec, pre, merge, ws, qs, npx = _schedule(lib, [1] * 256, k_lens, [k - 1 for k in k_lens], bt=bt, prefix=True)
     assert npx > 0 and len(merge) == 0
-    assert len(dec) <= 4096 and len(dec) % 16 == 0
-    loads = [sum(w["s1"] - w["s0"] for w in dec[g:g + 16] if w is not None) for g in range(0, len(dec), 16)]
+    assert len(dec) <= W * GROUPS and len(dec) % W == 0
+    loads = [sum(w["s1"] - w["s0"] for w in dec[g:g + W] if w is not None) for g in range(0, len(dec), W)]
     total = sum(-(-k // 16) - 64 for k in k_lens) * 8
     assert sum(loads) == total
     assert max(loads) <= total / len(loads) + 32  # within one tail of the mean
