@@ -13,22 +13,24 @@
 //    registers.  V^T is formed in registers with v_perm_b32 from 16-byte row
 //    loads.  Softmax statistics live in the lane that owns the m-row, so
 //    rescaling O needs no cross-lane traffic.
-//  * attn_decode_kernel<T, D, W>: rows with q_len == 1.  Decode time is set by
-//    the longest chain of dependent slice loads in any wave, so a row's keys
-//    are split over S = 1, 2, 4 or 8 waves per kv head (about
-//    KVHOT_SLICES_PER_WAVE slices each); a work-group of W = 8 waves serves
-//    W/S kv heads of one row and merges each head's S pieces through LDS.
-//    Only a row longer than one key partition stores (LSE, O) partials to
-//    HBM, combined by attn_merge_kernel in a second launch.  (Merging across
-//    work-groups inside one launch needs a device-scope release per wave,
-//    which on gfx950 is an L2 write-back per wave -- far slower than a launch;
-//    partial stores interleaved with the K/V stream also cost bandwidth, so
-//    they are kept to long rows.)
-//  * attn_prefill_kernel<T, D, NM>: rows with q_len >= 2.  A work-group of 4
-//    waves per (row, kv head, 4 blocks of 16*NM/G queries) stages 32-key K/V
-//    tiles through LDS and shares them; both products use the 16x16x32 MFMA
-//    (P^T keeps S^T's key order as the K dimension).  Causal mask from
-//    q_pos_offset; tiles past the work-group's last query are never loaded.
+//  * attn_decode_kernel<T, D, W>: rows with q_len == 1.  The host planner
+//    cuts every (row, kv head) into a segment of 16-token slices and packs
+//    the segments into work-groups of W = 8 waves, longest first, splitting a
+//    segment only where a work-group's load demands it.  Inside a work-group
+//    each wave claims slices one at a time from LDS counters and steals from
+//    the ranges with the most left, so waves that stream slower than their
+//    neighbours do not set the end time.  Per-(wave, segment) (LSE, O) pieces
+//    are merged through LDS; a segment split across work-groups stores
+//    partials to HBM that attn_merge_kernel combines in a second launch.  K/V
+//    loads are non-temporal: every byte of a call is read by one wave once.
+//  * attn_prefill_kernel<T, D, NM>: rows with q_len >= 2, and the key splits
+//    of a prefix shared by many decode rows (one unit serves all those rows'
+//    queries; the decode segments fold its partials in).  A work-group of 8
+//    waves per (row, kv head, query blocks) copies 32-key K/V tiles from the
+//    paged cache into LDS through a four-slot ring and shares them; both
+//    products use the 16x16x32 MFMA (P^T keeps S^T's key order as the K
+//    dimension).  Causal mask from q_pos_offset; tiles past the work-group's
+//    last query are never loaded.
 //  * attn_generic_kernel<T>: VALU kernel for fp32 (exact fp32 arithmetic) and
 //    for shapes the MFMA kernels do not cover.
 #include "kvhot_internal.h"
