@@ -1056,8 +1056,11 @@ attn_merge_kernel(const AttnArgs a) {
 // through a ring of four slots, three tiles ahead of the one being computed,
 // so each K/V byte is read from HBM once per work-group and from LDS once per
 // wave.  A wave skips tiles wholly past its own causal limit.
-constexpr int kPreWaves = 8;    // two per SIMD
-constexpr int kPreIssuers = 4;  // the leading wave of each SIMD
+#ifndef KVHOT_PRE_WAVES
+#define KVHOT_PRE_WAVES 8
+#endif
+constexpr int kPreWaves = KVHOT_PRE_WAVES;  // 8: two per SIMD
+constexpr int kPreIssuers = 4;              // the leading wave of each SIMD
 constexpr int kPreKeys = 32;
 constexpr int kPreSlots = 4;
 
@@ -1562,7 +1565,10 @@ static Plan make_plan(int64_t rows, int64_t max_q, int64_t max_k, int64_t Hq,
 
 // 16-row tiles of (query, head) pairs per prefill wave: O^T takes 64 VGPRs
 // and Q 32 at every head_dim, so two waves fit on a SIMD.
-constexpr int prefill_nm(int64_t D) { return D == 64 ? 4 : (D == 128 ? 2 : 1); }
+#ifndef KVHOT_PRE_NM128
+#define KVHOT_PRE_NM128 2
+#endif
+constexpr int prefill_nm(int64_t D) { return D == 64 ? 4 : (D == 128 ? KVHOT_PRE_NM128 : 1); }
 
 // Decode work-groups the current device holds at once, times their waves
 // (one work-group on each of 256 CUs when no device can be queried).
@@ -1626,7 +1632,10 @@ constexpr double kDecodeRateGBs = 5500.0;
 // Kv heads stream at different rates: which HBM channels a head's rows hit
 // follows from the row's byte offset inside a token's [Hkv, D] row, and on
 // MI355X two of eight 256-byte offsets read about 16% slower in every XCD
-// (shifting the pool by 256 bytes moves the slow heads along).  A work-group
+// (shifting the pool by 256 bytes moves the slow heads along; the slow pair
+// is h and h + 4, and which pair it is changes from one process to the next:
+// heads 1 and 5 at 2.66 against 3.22 slices per us in one, 3 and 7 in
+// another).  A work-group
 // of one head's segments then ends late or early with its head; one that
 // holds a mix of heads averages the rates (its waves share the slices).  So
 // the packing below places a segment, among the up to kMixCandidates
