@@ -266,14 +266,16 @@ struct WaveAttn {
 
   // Issues the loads of one 16-token slice of kv head kvh: tokens bo..bo+15
   // of physical block id.
-  __device__ void load_slice(const AttnArgs& a, int kvh, int64_t id, int bo, KVSlice<D>& T) const {
+  // With live false the descriptors cover no bytes (zeros, no memory read).
+  __device__ void load_slice(const AttnArgs& a, int kvh, int64_t id, int bo, KVSlice<D>& T,
+                             bool live = true) const {
     // Per-lane byte offsets inside the slice; one descriptor per block, over
     // this kv head's rows and bounded by the block stride.
     const int k_lane = 2 * (n * static_cast<int>(a.k_st) + 8 * g);
     const st* kb = static_cast<const st*>(a.k) + static_cast<int64_t>(kvh) * a.k_sh + id * a.k_sb;
     const st* vb = static_cast<const st*>(a.v) + static_cast<int64_t>(kvh) * a.v_sh + id * a.v_sb;
-    const __amdgpu_buffer_rsrc_t kr = block_rsrc(kb, static_cast<int>(2 * a.k_sb));
-    const __amdgpu_buffer_rsrc_t vr = block_rsrc(vb, static_cast<int>(2 * a.v_sb));
+    const __amdgpu_buffer_rsrc_t kr = block_rsrc(kb, live ? static_cast<int>(2 * a.k_sb) : 0);
+    const __amdgpu_buffer_rsrc_t vr = block_rsrc(vb, live ? static_cast<int>(2 * a.v_sb) : 0);
     const int ks = 2 * bo * static_cast<int>(a.k_st);
     const int vs = 2 * bo * static_cast<int>(a.v_st);
 #pragma unroll
@@ -285,10 +287,13 @@ struct WaveAttn {
   }
 
   // The loads of load_slice from the slice's block bases kb, vb (uniform).
-  __device__ void load_slice_from(const AttnArgs& a, const st* kb, const st* vb, int bo, KVSlice<D>& T) const {
+  // With live false the descriptors cover no bytes: every lane reads zeros
+  // and no memory is touched, but the loads still count in vmcnt.
+  __device__ void load_slice_from(const AttnArgs& a, const st* kb, const st* vb, int bo, KVSlice<D>& T,
+                                  bool live = true) const {
     const int k_lane = 2 * (n * static_cast<int>(a.k_st) + 8 * g);
-    const __amdgpu_buffer_rsrc_t kr = block_rsrc(kb, static_cast<int>(2 * a.k_sb));
-    const __amdgpu_buffer_rsrc_t vr = block_rsrc(vb, static_cast<int>(2 * a.v_sb));
+    const __amdgpu_buffer_rsrc_t kr = block_rsrc(kb, live ? static_cast<int>(2 * a.k_sb) : 0);
+    const __amdgpu_buffer_rsrc_t vr = block_rsrc(vb, live ? static_cast<int>(2 * a.v_sb) : 0);
     const int ks = 2 * bo * static_cast<int>(a.k_st);
     const int vs = 2 * bo * static_cast<int>(a.v_st);
 #pragma unroll
@@ -562,6 +567,12 @@ struct WaveAttn {
 // device-scope release per wave, which on gfx950 is an L2 write-back per wave
 // -- far slower than a launch.)
 
+// Slices in flight per decode wave: 1 (load the next slice after computing
+// this one) or 2 (double-buffered).
+#ifndef KVHOT_DECODE_DEPTH
+#define KVHOT_DECODE_DEPTH 1
+#endif
+
 #ifndef KVHOT_SLICES_PER_WAVE
 #define KVHOT_SLICES_PER_WAVE 8
 #endif
@@ -660,6 +671,12 @@ attn_decode_kernel(const AttnArgs a) {
       kend = ke_r;
       qs = a.q_starts[r];
       pidx = (static_cast<int64_t>(r) * a.Hkv + h) * a.max_parts + p;
+      // The first slice's block, as a launch list would give it.
+      const int64_t lb = (16 * static_cast<int64_t>(s0)) / a.bs;
+      if (s1 > s0 && lb < a.bt_stride) {
+        const int64_t id = a.bt[static_cast<int64_t>(r) * a.bt_stride + lb];
+        d_first = static_cast<int>(id < 0 ? 0 : (id >= a.num_blocks ? a.num_blocks - 1 : id));
+      }
     }
   }
   row = __builtin_amdgcn_readfirstlane(row);
@@ -700,9 +717,11 @@ attn_decode_kernel(const AttnArgs a) {
   KVSlice<D> T;
   int i = s0;              // slice whose loads are in flight, if `have`
   bool have = nsl > 0;     // the first slice of the range is taken without a claim
+#if KVHOT_DECODE_DEPTH < 2
   if (have)
     wa.load_slice(a, kvh, d_first >= 0 ? min(static_cast<int64_t>(d_first), a.num_blocks - 1) : block_of(row, s0),
                   kb % bs, T);
+#endif
   if (lane == 0) {
     cnt[wave] = s0 + (have ? 1 : 0);
     dend[wave] = s0 + nsl;
@@ -761,6 +780,7 @@ attn_decode_kernel(const AttnArgs a) {
     }
   };
 
+#if KVHOT_DECODE_DEPTH < 2
   int cv = wave;           // range being claimed from
   bool live = nsl > 0;     // the current segment may still have slices
   for (;;) {
@@ -816,6 +836,104 @@ attn_decode_kernel(const AttnArgs a) {
     cv = v;
     live = true;
   }
+#else
+  // Two slices in flight per wave: the older in one buffer, the newer in the
+  // other, and the block-table entry of the next claimed slice (iz) loading
+  // behind them.  A half-step computes the older buffer, claims one more
+  // slice and issues its block-table load, then refills the computed buffer
+  // with iz.  iz's entry was loaded before the newer buffer's K/V, so waiting
+  // for it leaves that buffer in flight (vector loads complete in order).
+  KVSlice<D> T1;
+  int ix = i, iy = 0, iz = 0, zraw = 0;
+  bool hx = have, hy = false, hz = false;
+  int cv = wave;           // range being claimed from
+  bool live = nsl > 0;     // the current segment may still have slices
+  auto claim_next = [&]() {
+    hz = false;
+    int j = -1;
+    if (live) {
+      j = claim(cv);
+      while (j < 0) {
+        const int v = pick(true);
+        if (v < 0) break;
+        cv = v;
+        j = claim(cv);
+      }
+      live = j >= 0;
+    }
+    // The entry is loaded on every path (entry 0 of the row when nothing was
+    // claimed), so the vector loads of each half-step come in one order.
+    const int64_t lb = j >= 0 ? (16 * static_cast<int64_t>(j)) / bs : 0;
+    const int r = max(__builtin_amdgcn_readfirstlane(krow), 0);
+    const int64_t e = lb < a.bt_stride ? lb : a.bt_stride - 1;
+    zraw = a.bt[static_cast<int64_t>(r) * a.bt_stride + (e > 0 ? e : 0)];
+    iz = max(j, 0);
+    hz = j >= 0;
+  };
+  // Computes the older buffer X, then refills it with slice iz.  The refill is
+  // issued on every path (no bytes when nothing was claimed): the waits the
+  // compiler places before a compute then always leave the other buffer's
+  // loads in flight.
+  auto half = [&](KVSlice<D>& X, int& ix_, bool& hx_) {
+    if (hx_) {
+      wa.compute_slice(a, 16 * ix_, kkend, INT_MAX, X);
+      used = true;
+    }
+    const bool take = __builtin_amdgcn_readfirstlane(static_cast<int>(hz)) != 0;
+    const int j = __builtin_amdgcn_readfirstlane(iz);
+    const int64_t jr = __builtin_amdgcn_readfirstlane(zraw);
+    const int64_t jb = jr < 0 ? 0 : (jr >= a.num_blocks ? a.num_blocks - 1 : jr);
+    claim_next();
+    wa.load_slice_from(a, uniform_ptr(static_cast<const st*>(a.k) + static_cast<int64_t>(kkvh) * a.k_sh + jb * a.k_sb),
+                       uniform_ptr(static_cast<const st*>(a.v) + static_cast<int64_t>(kkvh) * a.v_sh + jb * a.v_sb),
+                       __builtin_amdgcn_readfirstlane((16 * j) % bs), X, take);
+    ix_ = j;
+    hx_ = take;
+  };
+  // Segment exhausted and both buffers computed: park its state, then take
+  // slices of another one.
+  auto next_segment = [&]() -> bool {
+    if (used) flush();
+    const int v = pick(false);
+    if (v < 0) return false;
+    if (used) {
+      int ns = 0;
+      if (lane == 0) ns = atomicAdd(nslot, 1);
+      ns = __builtin_amdgcn_readlane(ns, 0);
+      if (ns >= S) return false;
+      slot = ns;
+      if (lane == 0) skey[4 * slot] = -1;
+      used = false;
+    }
+    const int* d = info + kDecInfo * v;
+    krow = __builtin_amdgcn_readfirstlane(d[0]);
+    kkvh = __builtin_amdgcn_readfirstlane(d[1]);
+    kpart = __builtin_amdgcn_readfirstlane(d[2]);
+    kkend = __builtin_amdgcn_readfirstlane(d[5]);
+    wa.setup(a, lane, kkvh, __builtin_amdgcn_readfirstlane(d[4]), 0, 1, kkend - 1);
+    cv = v;
+    live = true;
+    claim_next();
+    // Both buffers are computed here: waiting for the new Q and block-table
+    // entry now costs nothing, and keeps the loop's waits (which must hold on
+    // every path into it) from draining the other buffer after each half-step.
+    __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));  // vmcnt(0)
+    return true;
+  };
+  // The slice after the range's first, then the first (taken without a
+  // claim) into T, always issued: the loads enter the loop in the order each
+  // half-step leaves them (a block-table entry, then a buffer's K/V).
+  claim_next();
+  {
+    const bool h0 = __builtin_amdgcn_readfirstlane(static_cast<int>(have && d_first >= 0)) != 0;
+    wa.load_slice(a, kvh, h0 ? min(static_cast<int64_t>(d_first), a.num_blocks - 1) : 0, kb % bs, T, h0);
+  }
+  for (;;) {
+    half(T1, iy, hy);
+    half(T, ix, hx);
+    if (!hx && !hy && !hz && !next_segment()) break;
+  }
+#endif
   __syncthreads();
 
   // ---- merge: the first wave of each segment combines the segment's slots ----
@@ -2250,6 +2368,13 @@ static int paged_attention_impl(
   a.l_st = lse ? lse_strides[0] : 0;
   a.l_sh = lse ? lse_strides[1] : 0;
   a.bt = block_table; a.bt_stride = bt_row_stride;
+  // A launch with no keys may have no table; the decode loop still reads one
+  // entry ahead of its claims (row 0, entry 0 when nothing is claimed), so
+  // k_lens, which every launch has, stands in for it.
+  if (!a.bt || a.bt_stride == 0) {
+    a.bt = k_lens;
+    a.bt_stride = 0;
+  }
   a.q_lens = q_lens; a.k_lens = k_lens; a.q_starts = q_starts; a.q_offs = q_pos_offsets;
   a.num_blocks = num_blocks;
   a.Hq = static_cast<int32_t>(num_q_heads);
