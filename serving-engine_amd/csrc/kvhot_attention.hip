@@ -1617,7 +1617,7 @@ constexpr int64_t kCuLdsBytes = 160 * 1024;
 
 // Waves per decode work-group: 8 (KVHOT_MAX_DECODE_WAVES=16 builds a 16-wave
 // variant for head_dim <= 128 when one slot per wave fits in 64 KiB of LDS).
-// At head_dim 128 the 8-wave kernel takes 145 VGPRs, so a CU holds one such
+// At head_dim 128 the 8-wave kernel takes 135 VGPRs, so a CU holds one such
 // work-group: with non-temporal K/V loads, 8 waves per CU streamed faster
 // than 16 (measured on MI355X, one box, 64-row GQA workload: 52.2 against
 // 54.1 us per call; 55.7 us with 16 waves and cached loads).
