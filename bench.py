@@ -6,47 +6,64 @@ workload (64 rows, ctx U[128, 2048], 32/8 heads, D=128, bf16, block 16, pool
 (kvhot_reshape_and_cache) and the split-K paged decode attention
 (kvhot_paged_attention) over that layer's pool.  Each layer has its own
 ~348 MB pool (11 GB in all), so a layer's K/V is never still resident in the
-256 MB Infinity Cache when it is read again.
+256 MB Infinity Cache when it is read again.  The pool is the drop-in's
+documented one, allocate_kv_cache()'s default: the reference's
+[L, 2, N, 16, Hkv, D] shape and indexing with each block stored as
+[Hkv, 16, D] (head-major); `reference_layout` is the same calls on the
+reference's token-major [16, Hkv, D] blocks (--layout reference makes that
+the headline).
 
 value = algorithmic bytes moved per step (K/V read + Q in + O out + block
 table + LSE out, plus the append's K/V read+write and slots) / step time, in
-GB/s (1e9).  prefill = the chunked-prefill rows of the mixed workload (8 x
-512-token chunks on contexts U[0, 4096], 32/8 heads, D=128, bf16): one
-attention call over them, FLOPs counted over visible (query, key) pairs only,
-against the 2.5 PFLOP/s dense bf16 MFMA peak (and the whole mixed batch of
-that workload, decode rows included, timed alongside).  engine = output
-tokens/s of greedy decode steps of a random-weight Llama-3.1-8B-shaped model
-(32 layers, hidden 4096, 32/8 heads, D=128, vocab 128256, bf16) whose
-attention is paged|hip over a paged pool, 64 sequences with contexts
-U[128, 2048] (the GQA decode workload's lengths; the context K/V are
-synthetic, every decode step runs the whole model; the step is recorded once
-in a HIP graph and replayed, and the eager step is reported beside it), with
-the same model on the host CPU (fewer layers, the reference's eager attention
-restated in oracle/eager.py) as its baseline.  roofline = one attention call alone (the decode launch, plus a
-merge launch when the plan cuts a row across work-groups): its algorithmic bytes over
-its average duration, timed with HIP events on the launch stream across
-replays of one recorded HIP graph of 32 back-to-back calls (device time per
-launch; the eager per-call time, host dispatch included, is reported beside
-it); `traffic` = the HBM bytes rocprofv3's FETCH_SIZE and
+GB/s (1e9).  roofline = one attention call alone (the decode launch, plus a
+merge launch when the plan cuts a row across work-groups): its algorithmic
+bytes over its average duration, timed with HIP events on the launch stream
+across replays of one recorded HIP graph of 32 back-to-back calls (device
+time per launch; the eager per-call time, host dispatch included, is
+reported beside it); `traffic` = the HBM bytes rocprofv3's FETCH_SIZE and
 WRITE_SIZE counters read for the same call, scaled by what they read for a
-copy of known size, as recorded in profiles/attention_decode_gqa64_traffic.md
-(null when that file is absent).  head_major_pool = the same attention calls
-on a copy of the pool stored block-wise as [Hkv, 16, D]
-(allocate_kv_cache(head_major=True); same shape, values and results; not the
-headline, which keeps the reference's layout).  cpu_baseline = the reference's eager
-PyTorch path (restated in oracle/eager.py) on this host's cores, on one layer
-of the same batch.  copy = kvhot_copy_blocks over the prefix-sharing
-workload's 256 copy-on-write pairs on a 32-layer pool (1 GiB read and written
-per launch), GB/s against 8 TB/s.  prefill.decode_rows = the mixed
-workload's 56 decode rows alone, GB/s.  host_step = host time per engine step
-of the metadata and of the attention launch list.  Every per-launch figure is
-a median over --kernel-reps HIP-event timings.
+copy of known size, as recorded in profiles/ (null when that file is
+absent).  deterministic = the same calls with deterministic=True
+(KVHOT_DETERMINISTIC: bitwise-repeatable results).
+
+Other legs, each one attention (or append) call timed the same way over
+its own layer pools:
+* append_large: the mixed workload's 4,152-token append (8 x 512-token
+  chunks + 56 decode tokens), GB/s of K/V read + written against 8 TB/s;
+* prefix: the prefix-sharing workload (256 decode rows sharing 64 blocks,
+  private tails U[64, 512]), GB/s on the unique K/V bytes (the shared prefix
+  once) and on the logical ones (every row's keys);
+* long_context: the long-context workload (16 rows x 32,768 tokens over a
+  40 GB pool, 512-token split-K partitions), GB/s;
+* prefill: the chunked-prefill rows of the mixed workload (8 x 512-token
+  chunks on contexts U[0, 4096]): one attention call over them, FLOPs
+  counted over visible (query, key) pairs only, against the 2.5 PFLOP/s
+  dense bf16 MFMA peak; the whole mixed batch and its 56 decode rows alone
+  are timed alongside;
+* copy: kvhot_copy_blocks over the prefix-sharing workload's 256
+  copy-on-write pairs on a 32-layer pool (1 GiB read and written per
+  launch);
+* engine: output tokens/s of greedy decode steps of a random-weight
+  Llama-3.1-8B-shaped model (32 layers, hidden 4096, 32/8 heads, D=128,
+  vocab 128256, bf16) whose attention is paged|hip over a paged pool, 64
+  sequences with contexts U[128, 2048] (synthetic context K/V, the whole
+  model every step; the step recorded once in a HIP graph and replayed, the
+  eager step beside it), with the same model on the host CPU (the
+  reference's eager attention restated in oracle/eager.py; 1, 2 and 4
+  layers, the per-layer time fitted) as its baseline;
+* cpu_baseline: the reference's eager PyTorch path (restated in
+  oracle/eager.py) on this host's cores, on one layer of the same batch;
+* host_step: host time per engine step of the metadata and of the attention
+  launch list.
+Every per-launch figure is a median over --kernel-reps HIP-event timings.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload 2]
-       python bench.py --copy-probe   # kvhot_copy_blocks of 256 MiB each way
-                                      # (counter calibration)
-       python bench.py --prefill-only # the prefill measurement alone
-       python bench.py --copy-only    # the copy-on-write block copy measurement alone
+       python bench.py --headline-only   # the step and its attention call only
+                                         # (counter runs)
+       python bench.py --copy-probe      # kvhot_copy_blocks of 256 MiB each way
+                                         # (counter calibration)
+       python bench.py --prefill-only    # the prefill measurement alone
+       python bench.py --copy-only       # the copy-on-write block copy alone
 """
 from __future__ import annotations
 
@@ -64,7 +81,12 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
 MFMA_BF16_PEAK_TFLOPS = 2500.0
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "attention_decode_gqa64_traffic.md")
+TRAFFIC_FILES = {
+    "reference": os.path.join(ROOT, "profiles", "attention_decode_gqa64_traffic.md"),
+    "head-major": os.path.join(ROOT, "profiles", "attention_decode_gqa64_headmajor_traffic.md"),
+}
+LAYOUT_NAMES = {"head-major": "head-major blocks [Hkv, 16, D] (allocate_kv_cache's default)",
+                "reference": "the reference's token-major blocks [16, Hkv, D]"}
 
 
 def parse():
@@ -73,23 +95,29 @@ def parse():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", type=int, default=2, choices=[2, 3, 4, 5])
-    ap.add_argument("--head-major", action="store_true",
-                    help="pool stored block-wise as [Hkv, block_size, D] (allocate_kv_cache(head_major=True))")
+    ap.add_argument("--layout", choices=["head-major", "reference"], default="head-major",
+                    help="pool blocks stored [Hkv, 16, D] (allocate_kv_cache's default) or the reference's "
+                         "[16, Hkv, D]")
     ap.add_argument("--layers", type=int, default=32)
     ap.add_argument("--partition-tokens", type=int, default=0)
     ap.add_argument("--kernel-reps", type=int, default=20,
                     help="timed passes over all layers for the per-launch figures (their median is reported)")
+    ap.add_argument("--headline-only", action="store_true",
+                    help="only the step and its attention call on the headline layout (for counter runs)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-prefill", action="store_true", help="skip the prefill MFMA measurement")
     ap.add_argument("--prefill-only", action="store_true",
                     help="only the prefill measurement (for counter runs); prints its JSON object")
+    ap.add_argument("--no-legs", action="store_true",
+                    help="skip the append_large, prefix and long_context legs")
     ap.add_argument("--no-engine", action="store_true", help="skip the engine tokens/s measurement")
     ap.add_argument("--no-copy", action="store_true", help="skip the copy-on-write block copy measurement")
     ap.add_argument("--copy-only", action="store_true",
                     help="only the copy-on-write block copy measurement; prints its JSON object")
     ap.add_argument("--engine-only", action="store_true", help="only the engine measurement")
     ap.add_argument("--engine-steps", type=int, default=16)
-    ap.add_argument("--engine-cpu-layers", type=int, default=2)
+    ap.add_argument("--engine-cpu-layers", type=str, default="1,2,4",
+                    help="layer counts of the CPU engine baseline (the per-layer time is fitted over them)")
     ap.add_argument("--cpu-seconds", type=float, default=20.0, help="budget for the CPU baseline sample")
     ap.add_argument("--copy-probe", action="store_true",
                     help="only run kvhot_copy_blocks over 256 MiB each way, 5 times (counter calibration)")
@@ -156,16 +184,43 @@ def cpu_model():
     return platform.processor() or platform.machine()
 
 
-def recorded_traffic(workload: int):
+def recorded_traffic(workload: int, layout: str):
     """HBM bytes per attention call recorded from the rocprofv3 counter runs
-    (a `traffic_bytes_per_call: N` line of TRAFFIC_FILE), for workload 2."""
-    if workload != 2 or not os.path.exists(TRAFFIC_FILE):
+    (a `traffic_bytes_per_call: N` line of the layout's file under
+    profiles/), for workload 2."""
+    path = TRAFFIC_FILES.get(layout)
+    if workload != 2 or path is None or not os.path.exists(path):
         return None
-    with open(TRAFFIC_FILE) as f:
+    with open(path) as f:
         for line in f:
             if line.strip().startswith("traffic_bytes_per_call:"):
                 return int(line.split(":", 1)[1].strip())
     return None
+
+
+def per_call_us(body, calls, reps, dev):
+    """(graph, eager) per-call device time of body(), which makes `calls`
+    back-to-back calls: medians over `reps` passes, run eagerly (host
+    dispatch included) and as replays of one recorded HIP graph of the pass
+    (device time per call: what a kernel trace's average is compared with)."""
+    import torch
+
+    torch.cuda.synchronize()
+    eager = median_pass_us(body, reps) / calls
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream(dev)
+    side.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(side):
+        body()  # every lazy set-up done before the recording
+    torch.cuda.current_stream(dev).wait_stream(side)
+    torch.cuda.synchronize()
+    with torch.cuda.graph(graph):
+        body()
+    graph.replay()
+    torch.cuda.synchronize()
+    us = median_pass_us(graph.replay, reps) / calls
+    del graph
+    return us, eager
 
 
 def copy_probe():
@@ -202,7 +257,7 @@ def main():
 
         torch.cuda.set_device(0)
         print(json.dumps({"engine": engine_measure(torch.device("cuda:0"), steps=args.engine_steps,
-                                                   cpu_layers=0 if args.no_cpu_baseline else args.engine_cpu_layers)}),
+                                                   cpu_layers=[] if args.no_cpu_baseline else cpu_layer_counts(args))}),
               flush=True)
         return
     if args.copy_only:
@@ -233,7 +288,8 @@ def main():
 
     w = wl.make_workload(args.workload)
     layers = args.layers if args.workload != 5 else 1  # the 40 GB pool is one layer's
-    t = wl.make_tensors(w, dev, num_layers=layers, head_major=args.head_major)
+    head_major = args.layout == "head-major"
+    t = wl.make_tensors(w, dev, num_layers=layers, head_major=head_major)
     cache = sea._PagedKVCache(t.kv_cache)
     meta = sea.build_paged_batch_metadata(w.scheduler_output(), device=dev)
     slots = meta["slot_mapping"]
@@ -241,9 +297,9 @@ def main():
     pt = args.partition_tokens or w.partition_tokens or None
     blocks = [cache.blocks(i) for i in range(layers)]
 
-    def attention(i):
-        return sea.paged_flash_attention(t.q, blocks[i][0], blocks[i][1], meta, w.num_q_heads,
-                                         w.num_kv_heads, scale, partition_tokens=pt)
+    def attention(i, bl=blocks, deterministic=False):
+        return sea.paged_flash_attention(t.q, bl[i][0], bl[i][1], meta, w.num_q_heads,
+                                         w.num_kv_heads, scale, partition_tokens=pt, deterministic=deterministic)
 
     def step():
         for i in range(layers):
@@ -268,70 +324,58 @@ def main():
     step_bytes = layers * (attn_bytes + append_bytes)
     value = step_bytes / (ms_per_step * 1e-3) / 1e9
 
-    # Attention and append alone: back-to-back launches over the layers, as
-    # eager calls (host dispatch included) and as replays of one recorded HIP
-    # graph of the same launches (device time per launch: the figure the
-    # kernel trace's average is compared with).
+    # Attention and append alone: back-to-back launches over the layers.
     reps = max(1, args.kernel_reps)
-
-    def per_launch_us(body):
-        """Median over `reps` passes of (pass time / layers), eager and as
-        replays of one recorded graph of the pass."""
-        torch.cuda.synchronize()
-        eager = median_pass_us(lambda: body(), reps) / layers
-        graph = torch.cuda.CUDAGraph()
-        side = torch.cuda.Stream(dev)
-        side.wait_stream(torch.cuda.current_stream(dev))
-        with torch.cuda.stream(side):
-            body()  # every lazy set-up done before the recording
-        torch.cuda.current_stream(dev).wait_stream(side)
-        torch.cuda.synchronize()
-        with torch.cuda.graph(graph):
-            body()
-        graph.replay()
-        torch.cuda.synchronize()
-        return median_pass_us(graph.replay, reps) / layers, eager
-
-    attn_us, attn_eager_us = per_launch_us(lambda: [attention(i) for i in range(layers)])
+    attn_us, attn_eager_us = per_call_us(lambda: [attention(i) for i in range(layers)], layers, reps, dev)
     attn_gbs = attn_bytes / (attn_us * 1e-6) / 1e9
-    append_us, append_eager_us = per_launch_us(
-        lambda: [cache.write(t.new_k, t.new_v, i, slots) for i in range(layers)])
+    append_us, append_eager_us = per_call_us(
+        lambda: [cache.write(t.new_k, t.new_v, i, slots) for i in range(layers)], layers, reps, dev)
 
-    # The same calls on a copy of the pool stored block-wise as [Hkv, 16, D]
-    # (allocate_kv_cache(head_major=True)): same shape, values and results.
-    head_major = None
-    if not args.head_major:
+    other = deterministic = None
+    if not args.headline_only:
+        # The same calls on a copy of the pool in the other block layout (same
+        # shape, values and results), and with deterministic=True.
+        other_layout = "reference" if head_major else "head-major"
         kv2 = sea.allocate_kv_cache(layers, w.num_blocks, w.num_kv_heads, w.head_dim, dtype=w.dtype,
-                                    device=dev, head_major=True)
+                                    device=dev, head_major=not head_major)
         kv2.copy_(t.kv_cache)
         blocks2 = [(kv2[i, 0], kv2[i, 1]) for i in range(layers)]
-        hm_us, _ = per_launch_us(lambda: [
-            sea.paged_flash_attention(t.q, blocks2[i][0], blocks2[i][1], meta, w.num_q_heads, w.num_kv_heads,
-                                      scale, partition_tokens=pt) for i in range(layers)])
+        o_us, _ = per_call_us(lambda: [attention(i, blocks2) for i in range(layers)], layers, reps, dev)
         del kv2, blocks2
-        hm_gbs = attn_bytes / (hm_us * 1e-6) / 1e9
-        head_major = {"pool_layout": "head-major blocks [Hkv, 16, D] (allocate_kv_cache(head_major=True))",
-                      "avg_launch_us": round(hm_us, 3), "achieved": round(hm_gbs, 2), "unit": "GB/s",
-                      "frac": round(hm_gbs / HBM_PEAK_GBS, 4)}
+        o_gbs = attn_bytes / (o_us * 1e-6) / 1e9
+        other = {"pool_layout": LAYOUT_NAMES[other_layout], "avg_launch_us": round(o_us, 3),
+                 "achieved": round(o_gbs, 2), "unit": "GB/s", "frac": round(o_gbs / HBM_PEAK_GBS, 4),
+                 "traffic": recorded_traffic(args.workload, other_layout)}
+        d_us, _ = per_call_us(lambda: [attention(i, deterministic=True) for i in range(layers)], layers, reps, dev)
+        d_gbs = attn_bytes / (d_us * 1e-6) / 1e9
+        deterministic = {"flag": "KVHOT_DETERMINISTIC (paged_flash_attention(..., deterministic=True))",
+                         "pool_layout": LAYOUT_NAMES[args.layout], "avg_launch_us": round(d_us, 3),
+                         "achieved": round(d_gbs, 2), "unit": "GB/s", "frac": round(d_gbs / HBM_PEAK_GBS, 4),
+                         "cost_vs_default": round(d_us / attn_us - 1.0, 4)}
 
-    host_cost = host_step_cost(sea, w, dev, pt)
-
-    prefill = None
-    if not args.no_prefill:
-        prefill = prefill_measure(sea, wl, dev, reps=max(1, args.kernel_reps))
+    host_cost = None if args.headline_only else host_step_cost(sea, w, dev, pt)
 
     cpu = None
-    if not args.no_cpu_baseline:
+    if not args.no_cpu_baseline and not args.headline_only:
         cpu = cpu_baseline(w, t, layer=0, budget_s=args.cpu_seconds, attn_bytes=attn_bytes + append_bytes)
 
+    desc = launch_list_desc(meta, w)
     del t, cache, blocks
     torch.cuda.empty_cache()
-    copy = None if args.no_copy else copy_measure(sea, wl, dev, reps=reps)
 
+    legs = {}
+    if not args.headline_only and not args.no_legs:
+        legs["append_large"] = append_leg(sea, wl, dev, reps)
+        legs["prefix"] = attention_leg(sea, wl, dev, 4, layers=16, reps=reps)
+        legs["long_context"] = attention_leg(sea, wl, dev, 5, layers=1, reps=max(3, reps // 2), calls=8)
+    prefill = None
+    if not args.no_prefill and not args.headline_only:
+        prefill = prefill_measure(sea, wl, dev, reps=reps)
+    copy = None if args.no_copy or args.headline_only else copy_measure(sea, wl, dev, reps=reps)
     engine = None
-    if not args.no_engine:
+    if not args.no_engine and not args.headline_only:
         engine = engine_measure(dev, steps=args.engine_steps,
-                                cpu_layers=0 if args.no_cpu_baseline else args.engine_cpu_layers)
+                                cpu_layers=[] if args.no_cpu_baseline else cpu_layer_counts(args))
 
     line = {
         "metric": "decode paged-attn HBM GB/s (% of 8 TB/s); engine output tokens/sec",
@@ -356,29 +400,32 @@ def main():
             "append_tokens": w.total_query,
             "partition_tokens": pt or "auto",
             "seed": w.seed,
-            "pool_layout": "head-major blocks [Hkv, 16, D]" if args.head_major else "the reference's [16, Hkv, D] blocks",
+            "pool_layout": LAYOUT_NAMES[args.layout],
         },
         "pct_of_hbm_peak": round(100.0 * value / HBM_PEAK_GBS, 2),
         "roofline": {
             "bound": "hbm",
-            "kernel": launch_list_desc(meta, w),
+            "kernel": desc,
             "achieved": round(attn_gbs, 2),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(attn_gbs / HBM_PEAK_GBS, 4),
-            "traffic": recorded_traffic(args.workload),
+            "traffic": recorded_traffic(args.workload, args.layout),
             "algorithmic_bytes_per_launch": attn_bytes,
             "avg_launch_us": round(attn_us, 3),
-            "avg_launch_us_timing": "HIP events over replays of one recorded graph of the 32 back-to-back calls",
+            "avg_launch_us_timing": f"HIP events over replays of one recorded graph of the {layers} back-to-back calls",
             "eager_call_us": round(attn_eager_us, 3),
+            "pool_layout": LAYOUT_NAMES[args.layout],
         },
-        "head_major_pool": head_major,
+        "reference_layout" if head_major else "head_major_pool": other,
+        "deterministic": deterministic,
         "append": {"avg_launch_us": round(append_us, 3), "eager_call_us": round(append_eager_us, 3),
                    "algorithmic_bytes": append_bytes,
                    "gbs": round(append_bytes / (append_us * 1e-6) / 1e9, 2)},
         "host_step": host_cost,
         "cpu_baseline": cpu,
     }
+    line.update(legs)
     if copy is not None:
         line["copy"] = copy
     if prefill is not None:
@@ -386,6 +433,75 @@ def main():
     if engine is not None:
         line["engine"] = engine
     print(json.dumps(line), flush=True)
+
+
+def cpu_layer_counts(args):
+    return [int(x) for x in args.engine_cpu_layers.split(",") if x.strip()]
+
+
+def append_leg(sea, wl, dev, reps, layers=16):
+    """The mixed workload's append (8 x 512-token chunks + 56 decode tokens:
+    4,152 tokens x 8 kv heads x 128 x bf16 for K and V) into `layers` layer
+    pools: per-call time, GB/s of K/V read + written (+ slots) against 8 TB/s."""
+    import torch
+
+    w = wl.make_workload(3)
+    t = wl.make_tensors(w, dev, num_layers=layers, head_major=True)
+    cache = sea._PagedKVCache(t.kv_cache)
+    slots = t.slot_mapping
+    us, eager = per_call_us(lambda: [cache.write(t.new_k, t.new_v, i, slots) for i in range(layers)],
+                            layers, reps, dev)
+    nbytes = w.append_bytes()
+    gbs = nbytes / (us * 1e-6) / 1e9
+    del t, cache
+    torch.cuda.empty_cache()
+    return {"workload": w.name, "kernel": "reshape_and_cache_kernel", "tokens": w.total_query,
+            "algorithmic_bytes": nbytes, "avg_launch_us": round(us, 3), "eager_call_us": round(eager, 3),
+            "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
+            "timing": f"HIP events over replays of one recorded graph of {layers} back-to-back appends "
+                      f"(one layer pool each), median of {reps}"}
+
+
+def attention_leg(sea, wl, dev, config, layers, reps, calls=None):
+    """One attention call of workload `config` on head-major pools: per-call
+    time over `calls` back-to-back calls cycling through `layers` layer pools,
+    GB/s of its algorithmic bytes (logical: every row's keys; unique: each
+    physical K/V byte once) against 8 TB/s."""
+    import torch
+
+    w = wl.make_workload(config)
+    t = wl.make_tensors(w, dev, num_layers=layers, head_major=True)
+    cache = sea._PagedKVCache(t.kv_cache)
+    meta = sea.build_paged_batch_metadata(w.scheduler_output(), device=dev)
+    blocks = [cache.blocks(i) for i in range(layers)]
+    scale = 1.0 / math.sqrt(w.head_dim)
+    pt = w.partition_tokens or None
+    calls = calls or layers
+
+    def body():
+        for c in range(calls):
+            kc, vc = blocks[c % layers]
+            sea.paged_flash_attention(t.q, kc, vc, meta, w.num_q_heads, w.num_kv_heads, scale, partition_tokens=pt)
+
+    us, eager = per_call_us(body, calls, reps, dev)
+    logical = w.decode_algorithmic_bytes()
+    unique = w.decode_algorithmic_bytes(unique=True)
+    desc = launch_list_desc(meta, w)
+    del t, cache, blocks
+    torch.cuda.empty_cache()
+    out = {"workload": w.name, "kernel": desc, "avg_call_us": round(us, 3), "eager_call_us": round(eager, 3),
+           "algorithmic_bytes": logical, "achieved": round(logical / (us * 1e-6) / 1e9, 2), "peak": HBM_PEAK_GBS,
+           "unit": "GB/s", "frac": round(logical / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+           "pool_layout": LAYOUT_NAMES["head-major"],
+           "timing": f"HIP events over replays of one recorded graph of {calls} back-to-back calls over "
+                     f"{layers} layer pool(s), median of {reps}"}
+    if unique != logical:
+        out["unique_bytes"] = unique
+        out["unique_achieved"] = round(unique / (us * 1e-6) / 1e9, 2)
+        out["unique_frac"] = round(unique / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)
+    if pt:
+        out["partition_tokens"] = pt
+    return out
 
 
 class _DecodeRow:
@@ -465,7 +581,7 @@ def _decode_batch(steps, seed=1002):
     return [int(c) for c in ctx], tables, n
 
 
-def engine_measure(dev, steps=16, warmup=2, cpu_layers=2):
+def engine_measure(dev, steps=16, warmup=2, cpu_layers=(1, 2, 4)):
     """Greedy decode steps of the random-weight Llama-3.1-8B-shaped model on
     paged|hip attention: output tokens/s over `steps` timed steps (metadata,
     append, attention, the whole forward and argmax each step), run eagerly
@@ -478,7 +594,7 @@ def engine_measure(dev, steps=16, warmup=2, cpu_layers=2):
     cfg = _llama_8b_config(layers)
     model = _random_llama(cfg, dev, sea.register_attention())
     ctx, tables, n = _decode_batch(2 * (warmup + steps))
-    kv = sea.allocate_kv_cache(layers, n, 8, 128, dtype=torch.bfloat16, device=dev)
+    kv = sea.allocate_kv_cache(layers, n, 8, 128, dtype=torch.bfloat16, device=dev)  # head-major blocks
     gen = torch.Generator(device=dev)
     gen.manual_seed(1002)
     for lyr in range(layers):  # synthetic context K/V, N(0, 1) / sqrt(128)
@@ -552,19 +668,20 @@ def engine_measure(dev, steps=16, warmup=2, cpu_layers=2):
     }
     del graph, model, kv, cache
     torch.cuda.empty_cache()
-    if cpu_layers > 0:
+    if cpu_layers:
         res["cpu_baseline"] = engine_cpu_baseline(cpu_layers, ctx, tables, n)
     return res
 
 
-def engine_cpu_baseline(num_layers, ctx, tables, n, steps=3):
+def engine_cpu_baseline(layer_counts, ctx, tables, n, steps=5):
     """The same decode step on the host CPU with the reference's eager paged
     attention (restated in oracle/eager.py, per-row form) as the attention
-    function: output tokens/s of that model with 1 and with `num_layers`
-    layers (median step time of `steps` steps after one warm-up each), and
-    from those two the tokens/s of the 32-layer model the GPU runs (a step is
-    a fixed part -- embedding, final norm, LM head, argmax -- plus one
-    per-layer part per layer, so t(32) = t(1) + 31 * (t(L) - t(1)) / (L - 1))."""
+    function: the median step time of `steps` steps (after one warm-up) of
+    the model with each layer count in `layer_counts`, and from those a
+    least-squares line t(L) = t0 + L * t_layer (a step is a fixed part --
+    embedding, final norm, LM head, argmax -- plus one part per layer),
+    which gives the output tokens/s of the 32-layer model the GPU runs."""
+    import numpy as np
     import torch
     from transformers import AttentionInterface
 
@@ -610,29 +727,31 @@ def engine_cpu_baseline(num_layers, ctx, tables, n, steps=3):
             t0 = time.perf_counter()
             step()
             times.append(time.perf_counter() - t0)
+        del model, kv, cache
         return statistics.median(times)
 
-    t1 = step_seconds(1)
-    tl = step_seconds(num_layers) if num_layers > 1 else t1
-    per_layer = (tl - t1) / (num_layers - 1) if num_layers > 1 else t1
-    t32 = t1 + 31 * per_layer
+    counts = sorted(set(int(x) for x in layer_counts))
+    meas = [step_seconds(c) for c in counts]
+    if len(counts) > 1:
+        slope, t0 = np.polyfit(np.array(counts, dtype=np.float64), np.array(meas), 1)
+    else:
+        slope, t0 = meas[0], 0.0
+    t32 = t0 + 32 * slope
     batch = len(ctx)
     return {
-        "tokens_per_s": round(batch / tl, 2),
         "tokens_per_s_at_32_layers": round(batch / t32, 2),
         "unit": "tokens/s",
         "cores": threads,
         "cpu_model": cpu_model(),
         "host_cpus": os.cpu_count(),
         "kind": "port",
-        "sample": f"1- and {num_layers}-layer models of the same shape on the host CPU (bf16, torch, {threads} "
-                  f"threads), batch {batch}, eager paged attention (per-row form), median of {steps} steps after "
-                  f"1 warm-up each: {t1 * 1e3:.0f} and {tl * 1e3:.0f} ms per step; 32 layers extrapolated "
-                  f"as t(1) + 31 x the per-layer time",
-        "layers": num_layers,
-        "ms_per_step": {"1_layer": round(t1 * 1e3, 2), f"{num_layers}_layers": round(tl * 1e3, 2),
-                        "32_layers_extrapolated": round(t32 * 1e3, 2)},
-        "ms_per_layer": round(per_layer * 1e3, 2),
+        "sample": f"{', '.join(map(str, counts))}-layer models of the same shape on the host CPU (bf16, torch, "
+                  f"{threads} threads), batch {batch}, eager paged attention (per-row form), median of {steps} steps "
+                  f"after 1 warm-up each; step time fitted as t0 + L x t_layer and evaluated at 32 layers",
+        "ms_per_step_measured": {f"{c}_layers": round(m * 1e3, 2) for c, m in zip(counts, meas)},
+        "ms_per_layer_fitted": round(slope * 1e3, 2),
+        "ms_fixed_part_fitted": round(t0 * 1e3, 2),
+        "ms_per_step_at_32_layers": round(t32 * 1e3, 2),
     }
 
 
@@ -649,7 +768,7 @@ def prefill_measure(sea, wl, dev, reps, layers=16):
     decode = dataclasses.replace(full, rows=[r for r in full.rows if not r.prefill])
     out = {}
     for key, w in (("prefill_rows", rows), ("decode_rows", decode), ("mixed_batch", full)):
-        t = wl.make_tensors(w, dev, num_layers=layers)
+        t = wl.make_tensors(w, dev, num_layers=layers, head_major=True)
         cache = sea._PagedKVCache(t.kv_cache)
         meta = sea.build_paged_batch_metadata(w.scheduler_output(), device=dev)
         blocks = [cache.blocks(i) for i in range(layers)]

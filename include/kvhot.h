@@ -40,6 +40,15 @@ enum {
   KVHOT_BF16 = 2
 };
 
+/* attn_flags bits of kvhot_paged_attention(_noalloc) and
+ * kvhot_paged_attention_schedule.  1 and 0 keep the meaning of the
+ * reference's is_causal argument (serving_engine/paged_attention_kernel.py:125). */
+enum {
+  KVHOT_CAUSAL = 1,        /* key j is visible to query i iff j <= q_pos_offset + i */
+  KVHOT_DETERMINISTIC = 2  /* bitwise-repeatable out and lse: decode waves walk their
+                              planned key ranges in order, with no run-time sharing */
+};
+
 /* Invalid-argument codes (negative return values). */
 enum {
   KVHOT_EINVAL = -1,       /* a size, stride, pointer or dtype is invalid */
@@ -135,8 +144,9 @@ int64_t kvhot_paged_attention_workspace_bytes(
 /*
  * Launch list ("schedule") for kvhot_paged_attention, built on the host from
  * HOST copies of q_lens, k_lens, q_starts, q_pos_offsets and the block table,
- * with the head counts, head_dim, block_size, is_causal and dtype the
- * attention call will get.  The (row, kv head) key ranges of decode rows are
+ * with the head counts, head_dim, block_size, attn_flags (KVHOT_CAUSAL; the
+ * KVHOT_DETERMINISTIC bit is accepted and does not change the plan) and dtype
+ * the attention call will get.  The (row, kv head) key ranges of decode rows are
  * laid end to end and cut into equal numbers of 16-token slices per decode
  * work-group, one device-full of work-groups; a range cut in two becomes
  * "parts" in different work-groups.  Units of 8 int32, in order:
@@ -149,8 +159,10 @@ int64_t kvhot_paged_attention_workspace_bytes(
  * keys of that common prefix are attended once, for all of those rows'
  * queries together, by prefix units on the MFMA prefill path; each row's
  * decode work-group then reads only its own tail and folds the prefix
- * partials into its output.  The first *num_prefix_units of the prefill
- * units are such prefix units (they run before the decode launch).
+ * partials into its output (a row whose tail is cut across work-groups
+ * has them folded in by its merge unit instead).  The first
+ * *num_prefix_units of the prefill units are such prefix units (they run
+ * before the decode launch).
  * partition_tokens > 0 (a multiple of 32 up to 2^20) first cuts every decode
  * row into partitions of that many keys, which are then never cut further;
  * 0 leaves the cuts to the planner.  *workspace_bytes receives the workspace
@@ -167,7 +179,7 @@ int64_t kvhot_paged_attention_schedule(
     const int32_t* q_pos_offsets, const int32_t* block_table,
     int64_t bt_row_stride, int64_t num_rows, int64_t num_q_heads, int64_t num_kv_heads,
     int64_t head_dim, int64_t block_size, int64_t partition_tokens,
-    int is_causal, int dtype, int32_t* units, int64_t capacity_units,
+    int attn_flags, int dtype, int32_t* units, int64_t capacity_units,
     int64_t* num_decode_units, int64_t* num_prefill_units,
     int64_t* num_merge_units, int64_t* workspace_bytes,
     int64_t* num_prefix_units);
@@ -178,7 +190,7 @@ int64_t kvhot_paged_attention_schedule(
  * n_k = k_lens[r], off = q_pos_offsets[r], and each query i < n_q (global
  * token t = q_starts[r] + i) and query head h:
  *   keys j in [0, n_k) are read through block_table[r, j / block_size];
- *   when is_causal, key j is visible iff j <= off + i;
+ *   with KVHOT_CAUSAL in attn_flags, key j is visible iff j <= off + i;
  *   out[t, h, :] = softmax_j(scale * q[t,h,:] . k_j) @ v_j   (fp32 accumulate)
  *   lse[t, h]    = natural-log logsumexp_j(scale * q[t,h,:] . k_j)
  * A query with no visible key gets out = 0 and lse = -inf.
@@ -190,13 +202,16 @@ int64_t kvhot_paged_attention_schedule(
  * exactly these lengths and sizes, with its four unit counts, the workspace
  * size it reported (schedule_workspace_bytes) and a workspace at least that
  * large (a shorter one fails with KVHOT_EWORKSPACE before any launch); or
- * NULL, and then partition_tokens (keys per
- * decode partition; 0 picks a size, otherwise a multiple of 32 up to 2^20)
- * and kvhot_paged_attention_workspace_bytes apply.  With a schedule, decode
- * waves of one work-group share out their slices at run time, so the
- * summation order, and with it the last bits of out and lse, can differ from
- * call to call.  lse may be NULL.  out has the dtype of q, k_cache and
- * v_cache; lse is fp32.  Replaces paged_flash_attention +
+ * NULL, and then partition_tokens (keys per decode partition; 0 picks a
+ * size, otherwise a multiple of 32 up to 2^20) and
+ * kvhot_paged_attention_workspace_bytes apply.  Decode waves of one
+ * work-group share out their slices at run time (the waves of a CU stream at
+ * different rates), so the summation order, and with it the last bits of out
+ * and lse, can differ from call to call; with KVHOT_DETERMINISTIC in
+ * attn_flags every wave walks its planned range alone and repeated calls
+ * give the same bits (the work-group then ends with its slowest wave).
+ * Other attn_flags bits are invalid.  lse may be NULL.  out has the dtype of
+ * q, k_cache and v_cache; lse is fp32.  Replaces paged_flash_attention +
  * paged_flash_fwd_kernel (serving_engine/paged_attention_kernel.py:16-160).
  */
 int kvhot_paged_attention(
@@ -210,7 +225,7 @@ int kvhot_paged_attention(
     const int32_t* q_pos_offsets, int64_t num_rows, int64_t total_query,
     int64_t max_q_len, int64_t max_k_len, int64_t num_q_heads,
     int64_t num_kv_heads, int64_t head_dim, int64_t block_size,
-    int64_t num_blocks, float scale, int is_causal, int dtype,
+    int64_t num_blocks, float scale, int attn_flags, int dtype,
     int64_t partition_tokens, const int32_t* schedule,
     int64_t num_decode_units, int64_t num_prefill_units,
     int64_t num_merge_units, int64_t num_prefix_units,
@@ -249,7 +264,7 @@ int kvhot_paged_attention_noalloc(
     const int32_t* q_pos_offsets, int64_t num_rows, int64_t total_query,
     int64_t max_q_len, int64_t max_k_len, int64_t num_q_heads,
     int64_t num_kv_heads, int64_t head_dim, int64_t block_size,
-    int64_t num_blocks, float scale, int is_causal, int dtype,
+    int64_t num_blocks, float scale, int attn_flags, int dtype,
     int64_t partition_tokens, const int32_t* schedule,
     int64_t num_decode_units, int64_t num_prefill_units,
     int64_t num_merge_units, int64_t num_prefix_units,

@@ -23,6 +23,10 @@ KVHOT_F32 = 0
 KVHOT_F16 = 1
 KVHOT_BF16 = 2
 
+# attn_flags bits
+KVHOT_CAUSAL = 1
+KVHOT_DETERMINISTIC = 2
+
 # Split-K partials kvhot_paged_attention_noalloc holds (KVHOT_NOALLOC_SCRATCH_BYTES).
 NOALLOC_SCRATCH_BYTES = 32 << 20
 

@@ -80,6 +80,10 @@ struct AttnArgs {
   const int4* sched;
   const int4* merge_units;  // schedule: two int4 per split decode segment
   int32_t dec_slots;  // LDS (LSE, O) slots of a decode work-group, >= its waves
+  // KVHOT_DETERMINISTIC: every decode wave walks exactly its planned range,
+  // in order (no claiming from other waves), so each partial sum, and with it
+  // out and lse, is the same bits on every call.
+  int32_t fixed;
 };
 
 __device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
@@ -561,6 +565,9 @@ struct WaveAttn {
 // (LSE, O) in an LDS slot: its own slot first, then slots from a pool of
 // `dec_slots - W` (when the pool is empty the wave stops taking new segments).
 // After a barrier the first wave of each segment merges that segment's slots.
+// With KVHOT_DETERMINISTIC (AttnArgs::fixed) a wave claims from its own range
+// only and stops when it is used up: slices are summed in the same order on
+// every call.
 // A segment that is one of several partitions of its row stores an (LSE, O)
 // partial to HBM instead, and attn_merge_kernel combines the partitions in a
 // second launch.  (Merging across work-groups inside one launch needs a
@@ -607,9 +614,11 @@ __device__ inline int wave_max_int(int x) {
   return x;
 }
 
+// One decode work-group: launch-list work-group bx (decode descriptors at
+// sched), or without a launch list grid work-group (bx, by, bz).
 template <class TT, int D, int W>
-__global__ void __launch_bounds__(64 * W)
-attn_decode_kernel(const AttnArgs a) {
+__device__ __attribute__((always_inline)) inline void decode_wg(const AttnArgs& a, const int4* sched, int bx, int by,
+                                                                int bz) {
   extern __shared__ float smem[];
   using st = uint16_t;
   // Wave-uniform values are pinned to SGPRs with readfirstlane: derived from
@@ -620,18 +629,19 @@ attn_decode_kernel(const AttnArgs a) {
   const int G = a.G;
   const int PT = a.part_tokens;
   const int S = a.dec_slots;
+  const bool fixed = a.fixed != 0;
 
   // ---- this wave's range: slices [s0, s1) of part `part` of (row, kvh) ----
   int row = -1, kvh = 0, s0 = 0, s1 = 0, part = 0, nparts = 0, kend = 0;
   int64_t qs = 0, pidx = 0;
   int d_first = -1;
-  if (a.sched) {
+  if (sched) {
     // (row | parts << 16, kvh | part << 16, s0, s1), (query token, visible
     // keys, physical block of slice s0 or -1, partial index).  part with bit
     // 15 set (kPrefixFold): the row's shared prefix left `parts` partials
     // from index pidx in an earlier launch; this segment, the rest of the
     // row, folds them in and writes the row's output.
-    const int4* u = a.sched + 2 * (static_cast<int64_t>(blockIdx.x) * W + wave);
+    const int4* u = sched + 2 * (static_cast<int64_t>(bx) * W + wave);
     const int4 u0 = u[0], u1 = u[1];
     const int x = __builtin_amdgcn_readfirstlane(u0.x);
     const int y = __builtin_amdgcn_readfirstlane(u0.y);
@@ -648,8 +658,8 @@ attn_decode_kernel(const AttnArgs a) {
     d_first = __builtin_amdgcn_readfirstlane(u1.z);
     pidx = __builtin_amdgcn_readfirstlane(u1.w);
   } else {
-    const int r = blockIdx.z;
-    const int p = blockIdx.y;
+    const int r = bz;
+    const int p = by;
     if (a.q_lens[r] != 1) return;
     const int ke_r = decode_visible_keys(a, r);
     const int np = max((ke_r + PT - 1) / PT, 1);
@@ -658,8 +668,8 @@ attn_decode_kernel(const AttnArgs a) {
     const int nsl = max((min(ke_r, kbeg + PT) - kbeg + 15) / 16, 0);
     const int Sp = decode_splits(nsl, W, a.Hkv);
     const int HW = W / Sp;
-    if (static_cast<int>(blockIdx.x) * HW >= a.Hkv) return;
-    const int h = blockIdx.x * HW + wave / Sp;
+    if (static_cast<int>(bx) * HW >= a.Hkv) return;
+    const int h = bx * HW + wave / Sp;
     const int split = wave % Sp;
     if (h < a.Hkv) {
       row = r;
@@ -787,7 +797,7 @@ attn_decode_kernel(const AttnArgs a) {
     int j = -1;
     if (live) {
       j = claim(cv);
-      while (j < 0) {
+      while (j < 0 && !fixed) {
         const int v = pick(true);
         if (v < 0) break;
         cv = v;
@@ -816,6 +826,7 @@ attn_decode_kernel(const AttnArgs a) {
     have = false;
     // Segment exhausted: park its state, then take slices of another one.
     if (used) flush();
+    if (fixed) break;
     const int v = pick(false);
     if (v < 0) break;
     if (used) {
@@ -853,7 +864,7 @@ attn_decode_kernel(const AttnArgs a) {
     int j = -1;
     if (live) {
       j = claim(cv);
-      while (j < 0) {
+      while (j < 0 && !fixed) {
         const int v = pick(true);
         if (v < 0) break;
         cv = v;
@@ -894,6 +905,7 @@ attn_decode_kernel(const AttnArgs a) {
   // slices of another one.
   auto next_segment = [&]() -> bool {
     if (used) flush();
+    if (fixed) return false;
     const int v = pick(false);
     if (v < 0) return false;
     if (used) {
@@ -1009,10 +1021,18 @@ attn_decode_kernel(const AttnArgs a) {
   }
 }
 
+template <class TT, int D, int W>
+__global__ void __launch_bounds__(64 * W)
+attn_decode_kernel(const AttnArgs a) {
+  decode_wg<TT, D, W>(a, a.sched, blockIdx.x, blockIdx.y, blockIdx.z);
+}
+
 // Combines the parts of split decode segments: (row, kv head) pieces that
 // ran in different work-groups and left (LSE, O) partials.  With a schedule,
 // work-group u takes merge unit u = (query token, kv head, parts, first
-// partial index), each lane 8 head_dim values of one of the G query heads;
+// partial index), (first extra partial, extra partials) -- the extras are the
+// key splits of a shared prefix the row reads, written by prefix units --
+// each lane 8 head_dim values of one of the G query heads;
 // the kMergeWaves waves of the work-group fold a share of the parts each and
 // combine their states through LDS.  Without one, the grid is (head_dim
 // chunks, rows) of one-wave work-groups, and a row's parts are the fixed
@@ -1026,14 +1046,19 @@ attn_merge_kernel(const AttnArgs a) {
   constexpr int CH = D / 8;
   const int G = a.G;
   const int wv = static_cast<int>(threadIdx.x >> 6), nwv = static_cast<int>(blockDim.x >> 6);
-  int64_t t, base;
-  int kvh, nparts, it0, step;
+  int64_t t, base, xbase = 0;
+  int kvh, nparts, xparts = 0, it0, step;
   if (a.merge_units) {
+    // (query token, kv head, parts, first partial), (first extra partial,
+    // extra partials, 0, 0): the extra ones are a shared prefix's key splits.
     const int4 u = a.merge_units[2 * static_cast<int64_t>(blockIdx.x)];
+    const int4 u1 = a.merge_units[2 * static_cast<int64_t>(blockIdx.x) + 1];
     t = u.x;
     kvh = u.y;
     nparts = u.z;
     base = u.w;
+    xbase = u1.x;
+    xparts = u1.y;
     it0 = threadIdx.x & 63;
     step = 64;
   } else {
@@ -1051,10 +1076,13 @@ attn_merge_kernel(const AttnArgs a) {
     step = G * CH;             // one item per lane
   }
   if (t < 0 || t >= a.total_q || kvh < 0 || kvh >= a.Hkv || nparts < 1 || base < 0 ||
-      base + nparts > a.num_partials)
+      base + nparts > a.num_partials || xparts < 0 || xbase < 0 || xbase + xparts > a.num_partials)
     return;
-  constexpr int kFew = 4;  // up to this many parts, every load is issued at once
-  if (nparts <= kFew && wv > 0) return;  // one wave folds a few parts
+  // Partial of the i-th input: the parts, then the extra ones.
+  const int total = nparts + xparts;
+  auto input = [&](int i) -> int64_t { return i < nparts ? base + i : xbase + (i - nparts); };
+  constexpr int kFew = 4;  // up to this many inputs, every load is issued at once
+  if (total <= kFew && wv > 0) return;  // one wave folds a few inputs
   __shared__ float part_state[kMergeWaves][64][10];  // max, sum, O (8 values) per wave and lane
   for (int it = it0; it < G * CH; it += step) {
     const int hh = it / CH;
@@ -1062,16 +1090,17 @@ attn_merge_kernel(const AttnArgs a) {
     float mmax = -INFINITY;
     f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
     float lsum = 0.f;
-    if (nparts <= kFew) {
+    if (total <= kFew) {
       float lv[kFew];
       f32x4 p0[kFew], p1[kFew];
 #pragma unroll
       for (int pp = 0; pp < kFew; ++pp) {
         lv[pp] = -INFINITY;
         p0[pp] = p1[pp] = f32x4{0.f, 0.f, 0.f, 0.f};
-        if (pp < nparts) {
-          lv[pp] = a.ws_lse[(base + pp) * G + hh];
-          const f32x4* src = reinterpret_cast<const f32x4*>(a.ws_o + ((base + pp) * G + hh) * D + 8 * c);
+        if (pp < total) {
+          const int64_t pi = input(pp);
+          lv[pp] = a.ws_lse[pi * G + hh];
+          const f32x4* src = reinterpret_cast<const f32x4*>(a.ws_o + (pi * G + hh) * D + 8 * c);
           p0[pp] = src[0];
           p1[pp] = src[1];
         }
@@ -1081,7 +1110,7 @@ attn_merge_kernel(const AttnArgs a) {
       if (mmax != -INFINITY) {
 #pragma unroll
         for (int pp = 0; pp < kFew; ++pp) {
-          const float w = pp < nparts ? fast_exp2(lv[pp] - mmax) : 0.f;
+          const float w = pp < total ? fast_exp2(lv[pp] - mmax) : 0.f;
           lsum += w;
           acc0 += w * p0[pp];
           acc1 += w * p1[pp];
@@ -1092,8 +1121,8 @@ attn_merge_kernel(const AttnArgs a) {
       // together, then folded in with the running max moved (long rows have
       // tens of parts, and a part-by-part loop waits for each load in turn).
       constexpr int kBatch = 8;
-      const int lo = static_cast<int>((static_cast<int64_t>(nparts) * wv) / nwv);
-      const int hi = static_cast<int>((static_cast<int64_t>(nparts) * (wv + 1)) / nwv);
+      const int lo = static_cast<int>((static_cast<int64_t>(total) * wv) / nwv);
+      const int hi = static_cast<int>((static_cast<int64_t>(total) * (wv + 1)) / nwv);
       for (int b0 = lo; b0 < hi; b0 += kBatch) {
         float lv[kBatch];
         f32x4 p0[kBatch], p1[kBatch];
@@ -1102,8 +1131,9 @@ attn_merge_kernel(const AttnArgs a) {
           lv[k] = -INFINITY;
           p0[k] = p1[k] = f32x4{0.f, 0.f, 0.f, 0.f};
           if (b0 + k < hi) {
-            lv[k] = a.ws_lse[(base + b0 + k) * G + hh];
-            const f32x4* src = reinterpret_cast<const f32x4*>(a.ws_o + ((base + b0 + k) * G + hh) * D + 8 * c);
+            const int64_t pi = input(b0 + k);
+            lv[k] = a.ws_lse[pi * G + hh];
+            const f32x4* src = reinterpret_cast<const f32x4*>(a.ws_o + (pi * G + hh) * D + 8 * c);
             p0[k] = src[0];
             p1[k] = src[1];
           }
@@ -1228,9 +1258,12 @@ __device__ inline void half_barrier() {
   __builtin_amdgcn_sched_barrier(0);
 }
 
+// One prefill work-group: launch-list unit bx (prefill units at sched), or
+// without a launch list grid work-group (bx, by, bz).
 template <class TT, int D, int NM>
-__global__ void __launch_bounds__(64 * kPreWaves)
-attn_prefill_kernel(const AttnArgs a) {
+__device__ __attribute__((always_inline)) inline void prefill_wg(const AttnArgs& a, const int4* sched, int bx, int by,
+                                                                 int bz) {
+  (void)by;
   using Tile = PreTile<D>;
   using WA = WaveAttn<TT, D, NM>;
   // Ring slots, K tile then V tile.  Separate arrays: the compiler can tell
@@ -1264,9 +1297,9 @@ attn_prefill_kernel(const AttnArgs a) {
   int64_t qs = 0;
   int q0g = 0;
   bool prefix = false;
-  if (a.sched) {
-    const int4 u = a.sched[2 * static_cast<int64_t>(blockIdx.x)];
-    const int4 u1 = a.sched[2 * static_cast<int64_t>(blockIdx.x) + 1];
+  if (sched) {
+    const int4 u = sched[2 * static_cast<int64_t>(bx)];
+    const int4 u1 = sched[2 * static_cast<int64_t>(bx) + 1];
     row = u.x;
     kvh = u.y;
     prefix = __builtin_amdgcn_readfirstlane(u1.y) > 0;
@@ -1281,9 +1314,9 @@ attn_prefill_kernel(const AttnArgs a) {
       qblk = u.z;
     }
   } else {
-    row = blockIdx.z;
-    kvh = blockIdx.x % a.Hkv;
-    qblk = blockIdx.x / a.Hkv;
+    row = bz;
+    kvh = bx % a.Hkv;
+    qblk = bx / a.Hkv;
   }
   row = __builtin_amdgcn_readfirstlane(row);
   kvh = __builtin_amdgcn_readfirstlane(kvh);
@@ -1513,6 +1546,32 @@ attn_prefill_kernel(const AttnArgs a) {
   }
 }
 
+template <class TT, int D, int NM>
+__global__ void __launch_bounds__(64 * kPreWaves)
+attn_prefill_kernel(const AttnArgs a) {
+  prefill_wg<TT, D, NM>(a, a.sched, blockIdx.x, blockIdx.y, blockIdx.z);
+}
+
+// ---------------------------------------------------------------- mixed --
+// A batch of prefill and decode rows in one launch: work-groups [0, n_pre)
+// are prefill units (longest first), the rest decode work-groups.  Work-groups
+// are dispatched in order, so every prefill unit starts before any decode
+// work-group, and the decode work-groups take the CUs the prefill tail leaves
+// idle.  (Two launches leave those CUs idle; two streams let decode
+// work-groups interleave with the prefill units and put their longest-first
+// order off.)  Both bodies run 8-wave work-groups; the launch holds the
+// prefill's static LDS ring and the decode's dynamic LDS.
+template <class TT, int D, int NM, int W>
+__global__ void __launch_bounds__(64 * kPreWaves)
+attn_mixed_kernel(const AttnArgs a, const int4* pre_units, int n_pre) {
+  static_assert(W == kPreWaves, "one work-group size for both bodies");
+  const int b = blockIdx.x;
+  if (b < n_pre)
+    prefill_wg<TT, D, NM>(a, pre_units, b, 0, 0);
+  else
+    decode_wg<TT, D, W>(a, a.sched, b - n_pre, 0, 0);
+}
+
 // ----------------------------------------------------------- VALU kernel --
 // One wave per (row, query, query head).  Lanes take 64 keys at a time for the
 // scores; for P.V each lane owns head_dim values lane, lane+64, ...
@@ -1632,12 +1691,25 @@ static int64_t decode_lds_limit(int W, int64_t G, int64_t D) {
   return decode_lds_words(W, W, G, D) * 4 <= kMaxLdsBytes ? kMaxLdsBytes : kCuLdsBytes;
 }
 
-// LDS slots of a decode work-group of W waves: one per wave plus a pool of up
-// to W more for waves that move on to other segments, as LDS allows.
-static int decode_slots(int W, int64_t G, int64_t D) {
-  const int64_t spare = decode_lds_limit(W, G, D) / 4 - decode_lds_words(W, W, G, D);
+// LDS slots of a decode work-group of W waves in `limit` bytes of LDS: one per
+// wave plus a pool of up to W more for waves that move on to other segments,
+// as LDS allows; 0 when one slot per wave does not fit.
+static int decode_slots_within(int W, int64_t G, int64_t D, int64_t limit) {
+  const int64_t base = decode_lds_words(W, W, G, D);
+  if (base * 4 > limit) return 0;
+  const int64_t spare = limit / 4 - base;
   const int64_t per_slot = G * D + G + 4;
   return W + static_cast<int>(std::max<int64_t>(0, std::min<int64_t>(W, spare / per_slot)));
+}
+
+static int decode_slots(int W, int64_t G, int64_t D) {
+  return decode_slots_within(W, G, D, decode_lds_limit(W, G, D));
+}
+
+// Static LDS of a prefill work-group: the four-slot ring of K and V tiles.
+template <int D>
+constexpr int64_t prefill_ring_bytes() {
+  return static_cast<int64_t>(kPreSlots) * 2 * PreTile<D>::BYTES;
 }
 
 // Bytes of one split-K partial: the normalised O and LSE of G query heads.
@@ -1813,6 +1885,11 @@ static std::vector<PrefixGroup> find_prefix_groups(const int32_t* q_starts, cons
       int64_t l = 0;
       while (l < lim && bt[r * bt_stride + l] == bt[e * bt_stride + l]) ++l;
       if (l * bs < kMinPrefixKeys) break;
+      // n rows sharing lcp blocks read them once instead of n times.  A row
+      // that would shorten the prefix joins a group that is already large
+      // enough only if the group then saves more block reads.
+      const int64_t n = e - r;
+      if (l < lcp && n >= kMinPrefixRows && n * l <= (n - 1) * lcp) break;
       lcp = l;
       ++e;
     }
@@ -1918,11 +1995,10 @@ static bool plan_decode(const int32_t* q_lens, const int32_t* k_lens, const int3
       seg_kvh.push_back(static_cast<int>(h));
     }
     if (pfx_splits[r] > 0) {
-      // The row's own keys, whole, folding in the prefix's ks partials.
-      for (int64_t h = 0; h < Hkv; ++h) {
-        place(seg0 + static_cast<int>(h), r, h, pfx_sl[r], n - pfx_sl[r], kPrefixFold, false);
-        seg_parts[seg0 + h] = static_cast<int>(pfx_splits[r]);
-      }
+      // The row's own keys after the shared prefix.  Cut like any other
+      // segment: a segment left whole folds the prefix's partials in itself
+      // (kPrefixFold); the parts of a cut one meet them in its merge unit.
+      for (int64_t h = 0; h < Hkv; ++h) place(seg0 + static_cast<int>(h), r, h, pfx_sl[r], n - pfx_sl[r], 0, true);
     } else if (pt_sl > 0) {
       // Fixed partitions, partition-major over the row's kv heads: a
       // work-group's run of partitions spans the heads, whose streaming
@@ -1941,12 +2017,12 @@ static bool plan_decode(const int32_t* q_lens, const int32_t* k_lens, const int3
 
   // Uncut plan: whole segments, longest first, onto the least loaded of
   // `groups` work-groups.  Taken when the cut plan cut a segment and the
-  // uncut one is within a merge launch of balanced, and always when only
-  // fold segments (which the cut plan never cuts, closing work-groups early
-  // instead) are in the way.
+  // uncut one is within a merge launch of balanced, and when segments that
+  // fold shared-prefix partials are in the plan and nothing was cut (its
+  // packing mixes kv heads; see kMixCandidates).
   bool any_cut = false, any_fold = false;
   for (size_t sg = 0; sg < seg_parts.size(); ++sg) {
-    any_cut = any_cut || (seg_parts[sg] > 1 && pfx_splits[seg_row[sg]] == 0);
+    any_cut = any_cut || seg_parts[sg] > 1;
     any_fold = any_fold || pfx_splits[seg_row[sg]] > 0;
   }
   if (given_pt == 0 && (any_cut || any_fold)) {
@@ -1989,8 +2065,7 @@ static bool plan_decode(const int32_t* q_lens, const int32_t* k_lens, const int3
       }
       auto [ld, g2] = cand[c];
       const int64_t s0 = pfx_sl[seg_row[sg]];
-      lpt[g2].push_back(Piece{seg_row[sg], seg_kvh[sg], static_cast<int>(s0), static_cast<int>(s0 + n[sg]),
-                              pfx_splits[seg_row[sg]] > 0 ? kPrefixFold : 0, sg});
+      lpt[g2].push_back(Piece{seg_row[sg], seg_kvh[sg], static_cast<int>(s0), static_cast<int>(s0 + n[sg]), 0, sg});
       ++held[g2 * Hkv + h];
       ld += n[sg];
       lmax = std::max(lmax, ld);
@@ -2004,30 +2079,37 @@ static bool plan_decode(const int32_t* q_lens, const int32_t* k_lens, const int3
       wgs.clear();
       for (auto& g2 : lpt)
         if (!g2.empty()) wgs.push_back(std::move(g2));
-      for (int sg = 0; sg < nseg; ++sg) {
-        const int64_t ks = pfx_splits[seg_row[sg]];
-        seg_parts[sg] = ks > 0 ? static_cast<int>(ks) : 1;
-      }
+      std::fill(seg_parts.begin(), seg_parts.end(), 1);
     }
   }
 
-  // Partial indices of split segments (merged by merge units) and of the
-  // prefix partials a fold segment reads.
-  std::vector<int64_t> seg_base(seg_parts.size(), -1);
+  // Partial indices: first the prefix partials of every segment whose row
+  // shares a prefix (ks per segment, so the rows of a group lie at a fixed
+  // stride, as the prefix units write them), then the parts of cut segments.
+  // A cut segment's merge unit is (query token, kv head, parts, first part
+  // partial), (first prefix partial, ks, 0, 0) -- ks 0 when its row shares
+  // none.  A segment left whole that shares a prefix folds its ks prefix
+  // partials itself.
+  std::vector<int64_t> seg_base(seg_parts.size(), -1), pfx_base(seg_parts.size(), -1);
   for (size_t sg = 0; sg < seg_parts.size(); ++sg) {
-    if (seg_parts[sg] > 32767) return false;  // bits 16-30 of a wave descriptor's first int
-    if (pfx_splits[seg_row[sg]] > 0) {
-      seg_base[sg] = partials;
-      partials += seg_parts[sg];
-      if (partials > 0x7fffffff) return false;
-    } else if (seg_parts[sg] > 1) {
-      seg_base[sg] = partials;
-      mrg.push_back(int4{q_starts[seg_row[sg]], seg_kvh[sg], seg_parts[sg], static_cast<int>(partials)});
-      mrg.push_back(int4{0, 0, 0, 0});
-      partials += seg_parts[sg];
-      if (partials > 0x7fffffff) return false;
+    const int64_t ks = pfx_splits[seg_row[sg]];
+    // both counts fill bits 16-30 of a wave descriptor's first int
+    if (seg_parts[sg] > 32767 || ks > 32767) return false;
+    if (ks > 0) {
+      pfx_base[sg] = partials;
+      partials += ks;
     }
   }
+  for (size_t sg = 0; sg < seg_parts.size(); ++sg) {
+    if (seg_parts[sg] > 1) {
+      seg_base[sg] = partials;
+      const int64_t ks = pfx_splits[seg_row[sg]];
+      mrg.push_back(int4{q_starts[seg_row[sg]], seg_kvh[sg], seg_parts[sg], static_cast<int>(partials)});
+      mrg.push_back(int4{ks > 0 ? static_cast<int>(pfx_base[sg]) : 0, static_cast<int>(ks), 0, 0});
+      partials += seg_parts[sg];
+    }
+  }
+  if (partials > 0x7fffffff) return false;
 
   // Shared-prefix units: (row holding the prefix, kv head, first key, end
   // key), (first query token, queries, partial of the first query, partial
@@ -2041,10 +2123,10 @@ static bool plan_decode(const int32_t* q_lens, const int32_t* k_lens, const int3
       const int64_t r = pg.r0 + b * prefix_queries;
       const int64_t nq = std::min(prefix_queries, pg.nrows - b * prefix_queries);
       for (int64_t h = 0; h < Hkv; ++h) {
-        const int64_t base = seg_base[seg_start[r] + h];
-        const int64_t stride = nq > 1 ? seg_base[seg_start[r + 1] + h] - base : 1;
+        const int64_t base = pfx_base[seg_start[r] + h];
+        const int64_t stride = nq > 1 ? pfx_base[seg_start[r + 1] + h] - base : 1;
         for (int64_t i = 0; i < nq; ++i)
-          if (seg_base[seg_start[r + i] + h] != base + i * stride) return false;
+          if (pfx_base[seg_start[r + i] + h] != base + i * stride) return false;
         for (int64_t k = 0; k < ks; ++k) {
           const int64_t k0 = kPreKeys * (tiles * k / ks), k1 = kPreKeys * (tiles * (k + 1) / ks);
           if (k1 <= k0) return false;
@@ -2068,18 +2150,21 @@ static bool plan_decode(const int32_t* q_lens, const int32_t* k_lens, const int3
     }
     for (int i = 0; i < k; ++i) {
       const Piece& pc = g[i];
-      const int nparts = seg_parts[pc.seg];
       const int n = pc.s1 - pc.s0;
       const int r = pc.row;
-      const bool fold = pc.part == kPrefixFold;
-      const int pidx = fold ? static_cast<int>(seg_base[pc.seg])
+      // A whole segment of a row that shares a prefix folds the prefix's
+      // partials: its descriptor carries their count and first index.
+      const bool fold = pfx_splits[r] > 0 && seg_parts[pc.seg] == 1;
+      const int nparts = fold ? static_cast<int>(pfx_splits[r]) : seg_parts[pc.seg];
+      const int part = fold ? kPrefixFold : pc.part;
+      const int pidx = fold ? static_cast<int>(pfx_base[pc.seg])
                             : (nparts > 1 ? static_cast<int>(seg_base[pc.seg] + pc.part) : 0);
       for (int j = 0; j < w[i]; ++j) {
         const int a0 = pc.s0 + static_cast<int>((static_cast<int64_t>(n) * j) / w[i]);
         const int a1 = pc.s0 + static_cast<int>((static_cast<int64_t>(n) * (j + 1)) / w[i]);
         const int64_t lb = 16 * static_cast<int64_t>(a0) / bs;
         const int first = (a0 < a1 && lb < bt_stride) ? bt[r * bt_stride + lb] : -1;
-        dec.push_back(int4{r | (nparts << 16), pc.kvh | (pc.part << 16), a0, a1});
+        dec.push_back(int4{r | (nparts << 16), pc.kvh | (part << 16), a0, a1});
         dec.push_back(int4{q_starts[r], static_cast<int>(kend[r]), first, pidx});
       }
     }
@@ -2128,51 +2213,9 @@ static void launch_decode(const AttnArgs& a, int64_t rows, int64_t n_dec, hipStr
   hipLaunchKernelGGL((attn_decode_kernel<TT, D, W>), grid, dim3(64 * W), lds, stream, da);
 }
 
-// A second stream per device, so a mixed batch's prefill launch (MFMA-bound,
-// long) and its decode launches (HBM-bound) can share the GPU: the prefill
-// work-groups are dispatched first and the decode work-groups take the CUs
-// the prefill tail frees.  Forked from and joined back into the caller's
-// stream with events (the call stays ordered on that stream, and the pattern
-// is the one stream capture records).  Default priority.
-struct AuxStream {
-  hipStream_t stream = nullptr;
-  hipEvent_t fork = nullptr, join = nullptr;
-};
-static std::mutex g_aux_mutex;
-constexpr int kMaxDevices = 64;
-static AuxStream g_aux[kMaxDevices];
-
-// The current device's aux stream, created on first use; null if that fails
-// (the caller then launches everything on its own stream).  Call with
-// g_aux_mutex held.
-static AuxStream* aux_stream() {
-  int dev = -1;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
-    (void)hipGetLastError();
-    return nullptr;
-  }
-  AuxStream& x = g_aux[dev];
-  if (!x.stream) {
-    hipStream_t st = nullptr;
-    hipEvent_t f = nullptr, j = nullptr;
-    if (hipStreamCreateWithFlags(&st, hipStreamNonBlocking) != hipSuccess ||
-        hipEventCreateWithFlags(&f, hipEventDisableTiming) != hipSuccess ||
-        hipEventCreateWithFlags(&j, hipEventDisableTiming) != hipSuccess) {
-      (void)hipGetLastError();
-      if (f) (void)hipEventDestroy(f);
-      if (st) (void)hipStreamDestroy(st);
-      return nullptr;
-    }
-    x.stream = st;
-    x.fork = f;
-    x.join = j;
-  }
-  return &x;
-}
-
 template <class TT, int D>
 static void launch_mfma(const AttnArgs& a, int waves, int64_t rows, int64_t max_q, int64_t n_dec,
-                        int64_t n_pre, int64_t n_merge, int64_t n_pfx, bool use_aux, hipStream_t stream) {
+                        int64_t n_pre, int64_t n_merge, int64_t n_pfx, hipStream_t stream) {
   constexpr int NM = prefill_nm(D);
   if (a.sched && n_pfx > 0) {
     // Shared-prefix units, the first n_pfx of the prefill section, before
@@ -2183,20 +2226,25 @@ static void launch_mfma(const AttnArgs& a, int waves, int64_t rows, int64_t max_
     hipLaunchKernelGGL((attn_prefill_kernel<TT, D, NM>), dim3(static_cast<uint32_t>(n_pfx)), dim3(64 * kPreWaves), 0,
                        stream, xa);
   }
-  const bool dec = !a.sched || n_dec > 0;
-  const bool pre = a.sched ? n_pre > n_pfx : max_q >= 2;
-  hipStream_t pre_stream = stream;
-  std::unique_lock<std::mutex> lock(g_aux_mutex, std::defer_lock);
-  AuxStream* aux = nullptr;
-  if (dec && pre && a.sched && use_aux) {
-    lock.lock();
-    aux = aux_stream();
-    if (aux && hipEventRecord(aux->fork, stream) == hipSuccess &&
-        hipStreamWaitEvent(aux->stream, aux->fork, 0) == hipSuccess) {
-      pre_stream = aux->stream;
-    } else {
-      (void)hipGetLastError();
-      aux = nullptr;
+  bool dec = !a.sched || n_dec > 0;
+  bool pre = a.sched ? n_pre > n_pfx : max_q >= 2;
+  if constexpr (D <= 128) {
+    // Prefill units and decode work-groups in one grid, when the prefill's
+    // LDS ring and a decode work-group's slots fit one CU's LDS together
+    // (never at head_dim 256, whose ring alone takes 128 KiB).
+    const int slots = decode_slots_within(waves, a.G, D, kCuLdsBytes - prefill_ring_bytes<D>());
+    if (dec && pre && a.sched && waves == kPreWaves && slots > 0) {
+      AttnArgs ma = a;
+      ma.dec_slots = slots;
+      const size_t lds = static_cast<size_t>(decode_lds_words(waves, slots, a.G, D) * 4);
+      auto* kern = &attn_mixed_kernel<TT, D, NM, kPreWaves>;
+      if (static_cast<int64_t>(lds) + prefill_ring_bytes<D>() > kMaxLdsBytes)
+        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                  static_cast<int>(lds));
+      const int64_t n_units = n_pre - n_pfx;
+      hipLaunchKernelGGL(kern, dim3(static_cast<uint32_t>(n_units + n_dec / waves)), dim3(64 * kPreWaves), lds, stream,
+                         ma, a.sched + 2 * (n_dec + n_pfx), static_cast<int>(n_units));
+      dec = pre = false;
     }
   }
   if (pre) {
@@ -2206,7 +2254,7 @@ static void launch_mfma(const AttnArgs& a, int waves, int64_t rows, int64_t max_
                         : dim3(static_cast<uint32_t>(a.Hkv * nqb), 1u, static_cast<uint32_t>(rows));
     AttnArgs pa = a;
     if (a.sched) pa.sched = a.sched + 2 * (n_dec + n_pfx);
-    hipLaunchKernelGGL((attn_prefill_kernel<TT, D, NM>), grid, dim3(64 * kPreWaves), 0, pre_stream, pa);
+    hipLaunchKernelGGL((attn_prefill_kernel<TT, D, NM>), grid, dim3(64 * kPreWaves), 0, stream, pa);
   }
   if (dec) {
     bool launched = false;
@@ -2220,15 +2268,10 @@ static void launch_mfma(const AttnArgs& a, int waves, int64_t rows, int64_t max_
 #endif
     if (!launched) launch_decode<TT, D, 8>(a, rows, n_dec, stream);
   }
-  if (a.sched ? n_merge > 0 : dec && a.max_parts > 1) {
+  if (a.sched ? n_merge > 0 : (!a.sched || n_dec > 0) && a.max_parts > 1) {
     dim3 mgrid = a.sched ? dim3(static_cast<uint32_t>(n_merge))
                          : dim3(static_cast<uint32_t>((a.Hq * (D / 8) + 63) / 64), static_cast<uint32_t>(rows));
     hipLaunchKernelGGL((attn_merge_kernel<TT, D>), mgrid, dim3(a.sched ? 64 * kMergeWaves : 64), 0, stream, a);
-  }
-  if (aux) {
-    // Join: the caller's stream waits for the prefill launch.  (Errors of
-    // these calls stay pending for the caller's launch check.)
-    if (hipEventRecord(aux->join, aux->stream) == hipSuccess) (void)hipStreamWaitEvent(stream, aux->join, 0);
   }
 }
 
@@ -2254,7 +2297,7 @@ extern "C" int64_t kvhot_paged_attention_schedule(
     const int32_t* q_lens, const int32_t* k_lens, const int32_t* q_starts,
     const int32_t* q_pos_offsets, const int32_t* block_table, int64_t bt_row_stride,
     int64_t num_rows, int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim,
-    int64_t block_size, int64_t partition_tokens, int is_causal, int dtype,
+    int64_t block_size, int64_t partition_tokens, int attn_flags, int dtype,
     int32_t* units, int64_t capacity_units, int64_t* num_decode_units,
     int64_t* num_prefill_units, int64_t* num_merge_units, int64_t* workspace_bytes,
     int64_t* num_prefix_units) {
@@ -2263,6 +2306,9 @@ extern "C" int64_t kvhot_paged_attention_schedule(
       block_size <= 0 || partition_tokens < 0 || num_q_heads % num_kv_heads != 0 ||
       dtype_size(dtype) == 0 || capacity_units < 0 || bt_row_stride < 0)
     return set_error(KVHOT_EINVAL, "paged_attention_schedule: bad sizes");
+  if (attn_flags & ~(KVHOT_CAUSAL | KVHOT_DETERMINISTIC))
+    return set_error(KVHOT_EINVAL, "paged_attention_schedule: unknown attn_flags bits");
+  const bool is_causal = (attn_flags & KVHOT_CAUSAL) != 0;
   if (num_rows > 65535 || num_q_heads > 65535)
     return set_error(KVHOT_EUNSUPPORTED, "paged_attention_schedule: rows or heads too large");
   if (num_rows > 0 && (!q_lens || !k_lens || !q_starts || !q_pos_offsets ||
@@ -2286,10 +2332,9 @@ extern "C" int64_t kvhot_paged_attention_schedule(
     const int64_t groups = resident_decode_waves(dtype, head_dim, pl.waves, G) / pl.waves;
     const int64_t prefix_queries = kPreWaves * 16 * prefill_nm(head_dim) / G;  // per prefill work-group
     if (plan_decode(q_lens, k_lens, q_pos_offsets, q_starts, block_table, bt_row_stride, block_size,
-                    num_rows, num_kv_heads, is_causal != 0, pl.waves, groups, partition_tokens,
+                    num_rows, num_kv_heads, is_causal, pl.waves, groups, partition_tokens,
                     32 * head_dim * dtype_size(dtype), prefix_queries, dec, mrg, pfx, partials)) {
-      plan_prefill(q_lens, k_lens, q_pos_offsets, num_rows, num_kv_heads, G, head_dim,
-                   is_causal != 0, pre);
+      plan_prefill(q_lens, k_lens, q_pos_offsets, num_rows, num_kv_heads, G, head_dim, is_causal, pre);
       pre.insert(pre.begin(), pfx.begin(), pfx.end());  // shared-prefix units first
     } else {  // counts beyond the descriptor fields: no schedule
       dec.clear();
@@ -2316,8 +2361,8 @@ extern "C" int64_t kvhot_paged_attention_schedule(
   return n_dec + n_pre + n_mrg;
 }
 
-// kvhot_paged_attention's body.  use_aux: a mixed batch's prefill may run on
-// the device's second stream (created on first use).
+// kvhot_paged_attention's body: validation, then the launches, all on the
+// caller's stream.
 static int paged_attention_impl(
     const void* q, const int64_t q_strides[3], const void* k_cache,
     const int64_t k_cache_strides[4], const void* v_cache,
@@ -2327,10 +2372,10 @@ static int paged_attention_impl(
     const int32_t* q_starts, const int32_t* q_pos_offsets, int64_t num_rows,
     int64_t total_query, int64_t max_q_len, int64_t max_k_len,
     int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim,
-    int64_t block_size, int64_t num_blocks, float scale, int is_causal,
+    int64_t block_size, int64_t num_blocks, float scale, int attn_flags,
     int dtype, int64_t partition_tokens, const int32_t* schedule,
     int64_t num_decode_units, int64_t num_prefill_units, int64_t num_merge_units,
-    int64_t num_prefix_units, int64_t schedule_workspace_bytes, void* workspace, int64_t workspace_bytes, bool use_aux,
+    int64_t num_prefix_units, int64_t schedule_workspace_bytes, void* workspace, int64_t workspace_bytes,
     void* stream) {
   clear_error();
   const int64_t es = dtype_size(dtype);
@@ -2341,6 +2386,8 @@ static int paged_attention_impl(
     return set_error(KVHOT_EINVAL, "paged_attention: bad sizes");
   if (num_q_heads % num_kv_heads != 0)
     return set_error(KVHOT_EINVAL, "paged_attention: num_q_heads % num_kv_heads != 0");
+  if (attn_flags & ~(KVHOT_CAUSAL | KVHOT_DETERMINISTIC))
+    return set_error(KVHOT_EINVAL, "paged_attention: unknown attn_flags bits");
   if (num_rows == 0 || total_query == 0 || max_q_len == 0) return 0;
   if (!q || !k_cache || !v_cache || !out || !q_lens || !k_lens || !q_starts ||
       !q_pos_offsets || !q_strides || !k_cache_strides || !v_cache_strides ||
@@ -2382,7 +2429,8 @@ static int paged_attention_impl(
   a.G = static_cast<int32_t>(num_q_heads / num_kv_heads);
   a.bs = static_cast<int32_t>(block_size);
   a.scale_log2 = scale * kLog2e;
-  a.causal = is_causal ? 1 : 0;
+  a.causal = (attn_flags & KVHOT_CAUSAL) ? 1 : 0;
+  a.fixed = (attn_flags & KVHOT_DETERMINISTIC) ? 1 : 0;
   a.D = static_cast<int32_t>(head_dim);
   a.total_q = total_query;
   const int64_t n_dec = schedule ? num_decode_units : 0;
@@ -2437,7 +2485,7 @@ static int paged_attention_impl(
       a.max_parts = pl.max_parts;
     }
 #define KVHOT_MFMA(TT, DD) \
-  launch_mfma<TT, DD>(a, pl.waves, num_rows, max_q_len, n_dec, n_pre, n_mrg, n_pfx, use_aux, s)
+  launch_mfma<TT, DD>(a, pl.waves, num_rows, max_q_len, n_dec, n_pre, n_mrg, n_pfx, s)
     if (dtype == KVHOT_BF16) {
       if (head_dim == 64) KVHOT_MFMA(BF16, 64);
       else if (head_dim == 128) KVHOT_MFMA(BF16, 128);
@@ -2473,16 +2521,16 @@ extern "C" int kvhot_paged_attention(
     const int32_t* q_starts, const int32_t* q_pos_offsets, int64_t num_rows,
     int64_t total_query, int64_t max_q_len, int64_t max_k_len,
     int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim,
-    int64_t block_size, int64_t num_blocks, float scale, int is_causal,
+    int64_t block_size, int64_t num_blocks, float scale, int attn_flags,
     int dtype, int64_t partition_tokens, const int32_t* schedule,
     int64_t num_decode_units, int64_t num_prefill_units, int64_t num_merge_units,
     int64_t num_prefix_units, int64_t schedule_workspace_bytes, void* workspace, int64_t workspace_bytes, void* stream) {
   return paged_attention_impl(q, q_strides, k_cache, k_cache_strides, v_cache, v_cache_strides, out, out_strides,
                               lse, lse_strides, block_table, bt_row_stride, q_lens, k_lens, q_starts,
                               q_pos_offsets, num_rows, total_query, max_q_len, max_k_len, num_q_heads,
-                              num_kv_heads, head_dim, block_size, num_blocks, scale, is_causal, dtype,
+                              num_kv_heads, head_dim, block_size, num_blocks, scale, attn_flags, dtype,
                               partition_tokens, schedule, num_decode_units, num_prefill_units, num_merge_units,
-                              num_prefix_units, schedule_workspace_bytes, workspace, workspace_bytes, true, stream);
+                              num_prefix_units, schedule_workspace_bytes, workspace, workspace_bytes, stream);
 }
 
 // ------------------------------------------------------------ no-alloc --
@@ -2492,11 +2540,15 @@ extern "C" int kvhot_paged_attention(
 // device address comes from hipGetSymbolAddress, once per device.
 static __device__ __align__(256) unsigned char scratch[KVHOT_NOALLOC_SCRATCH_BYTES];
 
+constexpr int kMaxDevices = 64;
 static std::mutex g_scratch_mutex;
 static void* g_scratch_addr[kMaxDevices];
 
 // Device address of the current device's `scratch`, looked up on the
-// device's first call.  0, or a positive hipError_t.
+// device's first call.  0, or a positive hipError_t.  That first call may come
+// while the caller's stream is being captured into a graph: the lookup is not
+// a stream operation, and it runs with this thread's capture mode relaxed so
+// that a global-mode capture does not treat it as an unsafe call.
 static int scratch_address(void** out) {
   int dev = -1;
   const hipError_t de = hipGetDevice(&dev);
@@ -2508,7 +2560,10 @@ static int scratch_address(void** out) {
   std::lock_guard<std::mutex> guard(g_scratch_mutex);
   if (!g_scratch_addr[dev]) {
     void* p = nullptr;
+    hipStreamCaptureMode mode = hipStreamCaptureModeRelaxed;
+    const bool exchanged = hipThreadExchangeStreamCaptureMode(&mode) == hipSuccess;
     const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (exchanged) (void)hipThreadExchangeStreamCaptureMode(&mode);
     if (e != hipSuccess || !p) {
       (void)hipGetLastError();
       return set_error(e != hipSuccess ? static_cast<int>(e) : static_cast<int>(hipErrorInvalidSymbol),
@@ -2530,7 +2585,7 @@ extern "C" int kvhot_paged_attention_noalloc(
     const int32_t* q_starts, const int32_t* q_pos_offsets, int64_t num_rows,
     int64_t total_query, int64_t max_q_len, int64_t max_k_len,
     int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim,
-    int64_t block_size, int64_t num_blocks, float scale, int is_causal,
+    int64_t block_size, int64_t num_blocks, float scale, int attn_flags,
     int dtype, int64_t partition_tokens, const int32_t* schedule,
     int64_t num_decode_units, int64_t num_prefill_units, int64_t num_merge_units,
     int64_t num_prefix_units, int64_t schedule_workspace_bytes, void* stream) {
@@ -2555,8 +2610,8 @@ extern "C" int kvhot_paged_attention_noalloc(
   return paged_attention_impl(q, q_strides, k_cache, k_cache_strides, v_cache, v_cache_strides, out, out_strides,
                               lse, lse_strides, block_table, bt_row_stride, q_lens, k_lens, q_starts,
                               q_pos_offsets, num_rows, total_query, max_q_len, max_k_len, num_q_heads,
-                              num_kv_heads, head_dim, block_size, num_blocks, scale, is_causal, dtype,
+                              num_kv_heads, head_dim, block_size, num_blocks, scale, attn_flags, dtype,
                               partition_tokens, schedule, num_decode_units, num_prefill_units, num_merge_units,
                               num_prefix_units, schedule_workspace_bytes, ws, need > 0 ? int64_t{KVHOT_NOALLOC_SCRATCH_BYTES} : 0,
-                              false, stream);
+                              stream);
 }

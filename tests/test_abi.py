@@ -87,6 +87,13 @@ def test_attention_rejects_bad_arguments(lib):
     bad = list(args)
     bad[1] = _i64(4096, 128, 2)  # head_dim stride
     assert lib.kvhot_paged_attention(*bad) == -1
+    bad = list(args)
+    bad[26] = 4  # attn_flags: only KVHOT_CAUSAL (1) and KVHOT_DETERMINISTIC (2) exist
+    assert lib.kvhot_paged_attention(*bad) == -1
+    assert b"attn_flags" in lib.kvhot_last_error()
+    det = list(args)
+    det[26] = 3  # causal + deterministic: valid, so it gets as far as the workspace check
+    assert lib.kvhot_paged_attention(*det) == -3
     # split-K plan needs a workspace: none given -> KVHOT_EWORKSPACE (-3), before any launch
     assert lib.kvhot_paged_attention(*args) == -3
     assert b"workspace" in lib.kvhot_last_error()
@@ -394,14 +401,59 @@ def test_schedule_empty_for_vector_path(lib):
 FOLD = 0x8000  # part field of a decode segment that folds in shared-prefix partials
 
 
+def _shared_prefix_segments(dec, merge, qs, rows, k_lens, hkv, shared_blocks, ks):
+    """Checks the decode segments of a schedule with shared prefixes and
+    returns {(row, kv head): first prefix partial} for the rows in `rows`
+    (those that share `shared_blocks` blocks).  Such a segment covers the
+    row's tail only.  Left whole, it folds the prefix partials itself
+    (part FOLD, parts field ks, partial index = first prefix partial); cut,
+    its parts are ordinary parts and its merge unit names the prefix
+    partials as its extra inputs (first, ks).  Other rows start at key 0."""
+    units = {}
+    for qtok, kvh, n, b, xb, xn, z0, z1 in merge.tolist():
+        assert z0 == 0 and z1 == 0
+        units[(qtok, kvh)] = (n, b, xb, xn)
+    segs = {}
+    for g0 in range(0, len(dec), W):
+        for wv in dec[g0:g0 + W]:
+            if wv is not None:
+                segs.setdefault((wv["row"], wv["kvh"]), []).append((g0, wv))
+    pidx_of, cut = {}, 0
+    for (row, h), waves in segs.items():
+        waves.sort(key=lambda t: t[1]["s0"])
+        n = -(-k_lens[row] // 16)
+        assert waves[-1][1]["s1"] == n
+        assert all(a[1]["s1"] == b[1]["s0"] for a, b in zip(waves, waves[1:]))
+        parts = {w["part"] for _, w in waves}
+        if row in rows:
+            assert waves[0][1]["s0"] == shared_blocks  # the tail only
+            if parts == {FOLD}:
+                assert len({g for g, _ in waves}) == 1, "a folding segment cut across work-groups"
+                assert {w["nparts"] for _, w in waves} == {ks}
+                (pidx,) = {w["pidx"] for _, w in waves}
+                pidx_of[(row, h)] = pidx
+            else:
+                cut += 1
+                np_ = len(parts)
+                assert parts == set(range(np_)) and np_ > 1
+                nm, base, xb, xn = units.pop((int(qs[row]), h))
+                assert nm == np_ and xn == ks
+                assert {w["pidx"] for _, w in waves} == set(range(base, base + np_))
+                pidx_of[(row, h)] = xb
+        else:
+            assert waves[0][1]["s0"] == 0
+            assert FOLD not in parts
+    return pidx_of, cut
+
+
 def test_schedule_shared_prefix_units(lib):
     """Decode rows whose block tables start with the same blocks: the common
     prefix is attended by prefix units (the first units of the prefill
     section) once per query block, cut into key splits that tile it; each
-    row's decode segment starts after the prefix, is never cut across
-    work-groups, and names the partials the splits write for its query,
-    which no other unit uses.  Rows below the group size, or a prefill row
-    between decode rows, get no prefix."""
+    row's decode segment starts after the prefix and folds the partials the
+    splits write for its query (itself, or through its merge unit when the
+    planner cut it), which no other unit uses.  Rows below the group size,
+    or a prefill row between decode rows, get no prefix."""
     import numpy as np
 
     hq, hkv, d, G = 32, 8, 128, 4
@@ -421,28 +473,7 @@ def test_schedule_shared_prefix_units(lib):
     pb = G * (d + 1) * 4
     nparts_total = ws // pb
     assert ws == nparts_total * pb
-    # decode segments of every (row, kv head)
-    segs = {}
-    for g0 in range(0, len(dec), W):
-        for wv in dec[g0:g0 + W]:
-            if wv is not None:
-                segs.setdefault((wv["row"], wv["kvh"]), []).append((g0, wv))
-    pidx_of = {}
-    for (row, h), waves in segs.items():
-        waves.sort(key=lambda t: t[1]["s0"])
-        n = -(-k_lens[row] // 16)
-        assert waves[-1][1]["s1"] == n
-        assert all(a[1]["s1"] == b[1]["s0"] for a, b in zip(waves, waves[1:]))
-        if 1 <= row <= 70:
-            assert waves[0][1]["s0"] == 70  # the tail only
-            assert len({g for g, _ in waves}) == 1, "a folding segment cut across work-groups"
-            assert {w["part"] for _, w in waves} == {FOLD}
-            assert {w["nparts"] for _, w in waves} == {ks}
-            (pidx,) = {w["pidx"] for _, w in waves}
-            pidx_of[(row, h)] = pidx
-        else:
-            assert waves[0][1]["s0"] == 0
-            assert all(w["part"] != FOLD for _, w in waves)
+    pidx_of, _ = _shared_prefix_segments(dec, merge, qs, set(range(1, 71)), k_lens, hkv, 70, ks)
     assert len(pidx_of) == 70 * hkv
     # prefix units: (row, kv head, k0, k1), (query token, queries, partial, stride)
     pfx = pre[:npx].reshape(-1, 2, 4)
@@ -461,7 +492,7 @@ def test_schedule_shared_prefix_units(lib):
         ranges.sort()
         assert ranges[0][0] == 0 and ranges[-1][1] == 1120 and len(ranges) == ks
         assert all(a[1] == b[0] for a, b in zip(ranges, ranges[1:]))
-    # split k of (row, h) writes partial pidx + k: exactly the ones the decode segment folds
+    # split k of (row, h) writes partial pidx + k: exactly the ones the row's decode folds
     by_row = {}
     for row, h, p in written:
         by_row.setdefault((row, h), []).append(p)
@@ -472,7 +503,60 @@ def test_schedule_shared_prefix_units(lib):
     merge_parts = [b + j for _, _, n, b, *_ in merge.tolist() for j in range(n)]
     allp = fold_parts + merge_parts
     assert len(set(allp)) == len(allp) and max(allp) < nparts_total
-    assert not any(q - int(qs[1]) in range(70) for q, *_ in merge.tolist())
+
+
+def test_schedule_long_rows_sharing_a_short_prefix_fill_the_device(lib):
+    """A few long rows whose tables share a short prefix: their tails are cut
+    across work-groups like unshared rows (the prefix partials join each cut
+    tail's merge unit), so the decode launch still fills a device's worth of
+    work-groups with even loads."""
+    import numpy as np
+
+    for nrows, shared in ((4, 32), (8, 16), (16, 24)):
+        k_lens = [16384] * nrows
+        mb = 16384 // 16
+        bt = np.arange(nrows * mb, dtype=np.int32).reshape(nrows, mb) + 1000
+        bt[:, :shared] = 7 + np.arange(shared)
+        dec, pre, merge, ws, qs, npx = _schedule(lib, [1] * nrows, k_lens, [k - 1 for k in k_lens], bt=bt,
+                                                 prefix=True)
+        assert npx > 0
+        ks = npx // 8  # one query block, 8 kv heads
+        ngroups = len(dec) // W
+        loads = [sum(w["s1"] - w["s0"] for w in dec[g:g + W] if w is not None) for g in range(0, len(dec), W)]
+        total = nrows * 8 * (mb - shared)
+        assert sum(loads) == total
+        assert ngroups >= GROUPS - 8, (nrows, ngroups)
+        assert max(loads) <= total / GROUPS + 16, (nrows, max(loads), total / GROUPS)
+        pidx_of, cut = _shared_prefix_segments(dec, merge, qs, set(range(nrows)), k_lens, 8, shared, ks)
+        assert cut > 0 and len(pidx_of) == nrows * 8
+        # every prefix partial a row needs is written by a prefix unit (query
+        # token = row here: one query per row from token 0)
+        written = set()
+        for (r0, h, k0, k1), (qtok, nq, base, stride) in pre[:npx].reshape(-1, 2, 4).tolist():
+            for i in range(nq):
+                written.add((qtok + i, h, base + i * stride))
+        for (row, h), p in pidx_of.items():
+            assert all((row, h, p + k) in written for k in range(ks))
+
+
+def test_schedule_prefix_group_keeps_the_longer_prefix(lib):
+    """8 rows sharing 4096 keys, then a row that shares only their first 256:
+    the ninth row does not join (it would cut every row's shared keys to
+    256), so the group keeps its 4096-key prefix."""
+    import numpy as np
+
+    k_lens = [5000] * 9
+    mb = -(-5000 // 16)
+    bt = np.arange(9 * mb, dtype=np.int32).reshape(9, mb) + 1000
+    bt[:8, :256] = 7 + np.arange(256)
+    bt[8, :16] = 7 + np.arange(16)
+    dec, pre, merge, ws, qs, npx = _schedule(lib, [1] * 9, k_lens, [k - 1 for k in k_lens], bt=bt, prefix=True)
+    ranges = {(k0, k1) for (r0, h, k0, k1) in pre[:npx].reshape(-1, 2, 4)[:, 0].tolist()}
+    assert min(k0 for k0, _ in ranges) == 0 and max(k1 for _, k1 in ranges) == 4096
+    assert 8 not in {w["row"] for w in dec if w is not None and w["part"] == FOLD}
+    # the ninth row reads all its keys itself
+    starts = [w["s0"] for w in dec if w is not None and w["row"] == 8]
+    assert min(starts) == 0
 
 
 def test_schedule_shared_prefix_needs_enough_keys(lib):
@@ -517,3 +601,20 @@ def test_schedule_shared_prefix_stays_within_one_device_fill(lib):
     total = sum(-(-k // 16) - 64 for k in k_lens) * 8
     assert sum(loads) == total
     assert max(loads) <= total / len(loads) + 32  # within one tail of the mean
+
+
+def test_schedule_attn_flags(lib):
+    """The schedule takes the attention call's attn_flags: the deterministic
+    bit leaves the plan as it is, unknown bits are rejected."""
+    import numpy as np
+
+    k_lens = [300, 1200, 17]
+    plans = [_schedule(lib, [1, 1, 1], k_lens, [k - 1 for k in k_lens], causal=c) for c in (1, 3)]
+    assert all(np.array_equal(a, b) for a, b in zip(plans[0][1:3], plans[1][1:3]))
+    assert plans[0][0] == plans[1][0] and plans[0][3] == plans[1][3]
+    q = np.ones(1, np.int32)
+    cnt = [ctypes.c_int64() for _ in range(5)]
+    got = lib.kvhot_paged_attention_schedule(q.ctypes.data, q.ctypes.data, q.ctypes.data, q.ctypes.data,
+                                             q.ctypes.data, 1, 1, 32, 8, 128, 16, 0, 8, 2, None, 0,
+                                             *(ctypes.byref(c) for c in cnt))
+    assert got == -1 and b"attn_flags" in lib.kvhot_last_error()

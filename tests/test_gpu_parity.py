@@ -539,3 +539,48 @@ def test_prefill_ring_tiles_distinct(cuda, sea, wl, hq, hkv, d):
     assert_attention(w, o, l, ref_o, ref_l)
     (plan,) = [p for p in meta["_schedules"].values() if p is not None]
     assert plan[5] > 0 and plan[2] > plan[5]  # prefix units and prefill rows ran
+
+
+@pytest.mark.parametrize("nrows,shared", [(4, 32), (16, 16)])
+def test_long_rows_sharing_a_short_prefix(cuda, sea, wl, nrows, shared):
+    """A few 16k-key rows sharing a short prefix: the prefix is attended once
+    by prefix units, and the rows' tails are cut across work-groups, their
+    merge units folding the prefix partials in as extra inputs (12 inputs per
+    unit with 4 rows, about 4 with 16)."""
+    spec = [(1, 16384, 16383)] * nrows
+    w = shared_custom(wl, spec, [(0, nrows, shared)], 32, 8, 128, torch.bfloat16, seed=31 + nrows)
+    announce(f"{nrows} rows x 16384 keys sharing {shared} blocks")
+    T = wl.make_tensors(w, cuda)
+    ref_o, ref_l = oracle_step(w, T)
+    meta = wl.metadata_tensors(w, cuda)
+    o, l = hip_step(sea, wl, w, T, meta=meta)
+    assert_attention(w, o, l, ref_o, ref_l)
+    (plan,) = [p for p in meta["_schedules"].values() if p is not None]
+    assert plan[5] > 0 and plan[3] > 0  # prefix units, and merge units for the cut tails
+
+
+
+@pytest.mark.parametrize("config,scheduled", [(2, True), (2, False), (3, True), (4, True)])
+def test_deterministic_calls_repeat_bitwise(cuda, sea, wl, config, scheduled):
+    """deterministic=True (KVHOT_DETERMINISTIC): two calls on the same inputs
+    give the same bits of out and lse -- decode with and without a launch
+    list, a mixed prefill + decode batch, and shared-prefix rows -- and both
+    match the oracle."""
+    w = wl.make_workload(config)
+    announce(f"deterministic attention, workload {config}, launch list={scheduled}")
+    T = wl.make_tensors(w, cuda)
+    ref_o, ref_l = oracle_step(w, T)
+    meta = wl.metadata_tensors(w, cuda)
+    if not scheduled:
+        meta = {k: v for k, v in meta.items() if not k.startswith("host_")}
+    cache = sea._PagedKVCache(T.kv_cache)
+    cache.write(T.new_k, T.new_v, 0, T.slot_mapping)
+    kc, vc = cache.blocks(0)
+    outs = []
+    for _ in range(2):
+        o, l = sea.paged_flash_attention(T.q, kc, vc, meta, w.num_q_heads, w.num_kv_heads,
+                                         1.0 / math.sqrt(w.head_dim), deterministic=True)
+        torch.cuda.synchronize()
+        outs.append((bits(o), l.cpu().numpy().view(np.int32)))
+    assert np.array_equal(outs[0][0], outs[1][0]) and np.array_equal(outs[0][1], outs[1][1])
+    assert_attention(w, o, l, ref_o, ref_l)
