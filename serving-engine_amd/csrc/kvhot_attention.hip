@@ -1357,8 +1357,7 @@ __device__ __attribute__((always_inline)) inline void prefill_wg(const AttnArgs&
   // half hw.  Lane L's chunk is physical chunk pc of row pr; it loads logical
   // chunk pc ^ swz(pr) of that key.
   constexpr int NI = Tile::NI;
-  const int grp = wave / kPreIssuers;  // 0 leads, 1 runs one half-step behind
-  const bool issuer = grp == 0;
+  const bool issuer = wave < kPreIssuers;
   const int hw = __builtin_amdgcn_readfirstlane(issuer ? (64 * NI * wave) / (16 * Tile::CPR) : 0);
   uint32_t koff[NI], voff[NI];
 #pragma unroll
@@ -1379,28 +1378,28 @@ __device__ __attribute__((always_inline)) inline void prefill_wg(const AttnArgs&
   const uint32_t ksb = 2u * static_cast<uint32_t>(a.k_sb), vsb = 2u * static_cast<uint32_t>(a.v_sb);
   const uint32_t kst = 2u * static_cast<uint32_t>(a.k_st), vst = 2u * static_cast<uint32_t>(a.v_st);
   const uint32_t nblocks = static_cast<uint32_t>(a.num_blocks);
-  // Block ids come through scalar loads (constant address space), fetched
-  // one tile ahead: nid is the physical block holding this wave's half of
-  // the next tile to load, at row nbo of logical block nblk.  (A vector load
-  // here would make the compiler wait for every DMA in flight before using
-  // it.)
+  // Block ids come through scalar loads (constant address space): nblk is
+  // the logical block holding this wave's half of the next tile to load,
+  // nbo its first row there.  (A vector load here would make the compiler
+  // wait for every DMA in flight before using it.  Staging the unit's ids in
+  // LDS before the first DMA instead measured the same.)
   const __attribute__((address_space(4))) int32_t* btc =
       (const __attribute__((address_space(4))) int32_t*)btrow;
   auto bt_at = [&](int blk) -> int { return btc[min(blk, max(nb_row - 1, 0))]; };
   int nblk = (k0 + 16 * hw) / bs, nbo = (k0 + 16 * hw) % bs;
-  int nid = issuer && nb_row > 0 ? bt_at(nblk) : 0;
 
   // DMA of tile t (the next in order) into ring slot S.  The descriptor of
   // the half starts at its first key and covers only keys below kend_g: the
   // rows past it read as zeros.
   auto issue = [&](int S, int t) {
+    const int nid = bt_at(nblk);
     const uint32_t b = min(static_cast<uint32_t>(max(nid, 0)), nblocks - 1);
     const int rows = min(max(kend_g - (k0 + kPreKeys * t + 16 * hw), 0), 16);
     const char* kb = kbase + (static_cast<uint64_t>(b) * ksb + static_cast<uint32_t>(nbo) * kst);
     const char* vb = vbase + (static_cast<uint64_t>(b) * vsb + static_cast<uint32_t>(nbo) * vst);
     const int nrk = __builtin_amdgcn_readfirstlane(rows * static_cast<int>(kst));
     const int nrv = __builtin_amdgcn_readfirstlane(rows * static_cast<int>(vst));
-    // This half of tile t + 1 (32 keys on), and its block id.
+    // This half of tile t + 1 (32 keys on).
     if (bs == 16) {
       nblk += 2;
     } else {
@@ -1410,7 +1409,6 @@ __device__ __attribute__((always_inline)) inline void prefill_wg(const AttnArgs&
         ++nblk;
       }
     }
-    nid = bt_at(nblk);
     char* dst = slot(S) + 1024 * NI * wave;
     const rsrc_words_t kr = rsrc_words(kb, nrk), vr = rsrc_words(vb, nrv);
 #pragma unroll
@@ -1420,23 +1418,16 @@ __device__ __attribute__((always_inline)) inline void prefill_wg(const AttnArgs&
     }
   };
 
-  // Ping-pong over half-steps.  Tile t is two half-steps: M(t), the MFMA
-  // work -- PV of tile t-1 and QK of tile t -- and X(t), the softmax of tile
-  // t.  Every half-step ends in one work-group barrier.  The second wave of
-  // each SIMD (group 1) runs one half-step behind the first (group 0), so
-  // while one is in its MFMA half-step the other is in its softmax: the
-  // matrix core and the VALU work side by side.  Group 1 passes one extra
-  // barrier first and group 0 one extra at the end, so both pass the same
-  // number.
-  //
-  // The DMA is group 0's scalar and issue work, kept out of its MFMA
-  // half-steps: in X(t), group 0 waits for its part of tile t+1 (read first
-  // in M(t+1), after the barrier that ends X(t)), then issues tile t+LEAD
-  // into the slot of tile t+LEAD-4, whose last reads are done: at LEAD 3 (V^T
-  // read in X), tile t-1's V^T in group 1's X(t-1), one half-step before;
-  // at LEAD 2 (D = 256 reads V^T in M), tile t-2's in group 1's M(t-1).  Tile
-  // t sits in slot t % 4; the loop body is unrolled four times so that every
-  // LDS access names a fixed slot.
+  // One phase per tile, each ending in one work-group barrier (see the
+  // loop below).  The issuing waves put tile t+LEAD in flight at the start
+  // of phase t; tile t sits in slot t % 4, and the loop body is unrolled
+  // four times so that every LDS access names a fixed slot.  (The two waves
+  // of a SIMD run the same phase and the hardware interleaves one's MFMAs
+  // with the other's softmax: a probe of this tile's MFMA, LDS and softmax
+  // work ran at 20 cycles per MFMA with one barrier per tile and 27 with
+  // the waves pinned half a tile apart by two barriers per tile; in this
+  // kernel the half-tile ping-pong measured 187.5 us against 182.6 on the
+  // mixed workload's prefill rows.)
   constexpr int PER_TILE = 2 * NI;  // DMA instructions per issuing wave and tile
   constexpr int LEAD = WA::NC <= 4 ? 3 : 2;
   const int ntiles = (kend_g - k0 + kPreKeys - 1) / kPreKeys;
@@ -1467,20 +1458,29 @@ __device__ __attribute__((always_inline)) inline void prefill_wg(const AttnArgs&
 #pragma unroll
   for (int s = 0; s < NM; ++s) wa.m[s] = -FLT_MAX;
   half_barrier();
-  if (grp == 1) half_barrier();
 
-  // LDS reads never wait inside a half-step: M(t) issues all of tile t's K
-  // reads first and runs PV(t-1) from registers while they land; X(t) reads
-  // tile t's V^T operands while the softmax runs, for PV(t) in M(t+1).  D =
-  // 256 (registers): K half a tile at a time, and tile t-1's V^T read in
-  // M(t) itself.
+  // A phase issues all of tile t's K reads first and runs PV(t-1) from
+  // registers while they land, and reads tile t's V^T operands for PV(t) in
+  // the next phase.  D = 256 (registers): K half a tile at a time, and tile
+  // t-1's V^T read in phase t itself.
   constexpr bool kVAhead = WA::NC <= 4;
   u32x4 pb[NM];           // P of the previous tile, for its PV
   u32x4 va[WA::VB];       // its V^T operands
   bool pv_due = false;    // the previous tile had keys this wave sees
+  // One phase per tile, ending in the tile's one barrier.  At its start the
+  // issuing waves put tile t+LEAD in flight, into the slot of tile t+LEAD-4:
+  // at LEAD 3 tile t-1's, whose K and V^T reads ended before the last
+  // barrier (PV(t-1) runs from registers); at LEAD 2 (D = 256, V^T read for
+  // PV(t-1) in this phase) tile t-2's.  Each wave then reads tile t's K, runs
+  // PV(t-1), QK(t), reads tile t's V^T and forms P(t).  Before the barrier an
+  // issuing wave waits for its part of tile t+1: its DMAs complete in issue
+  // order, and the only vector memory operations in the loop are these DMAs,
+  // so vmcnt <= (tiles in flight after t+1) * PER_TILE means tile t+1's
+  // PER_TILE instructions have landed.  The two waves of a SIMD run the same
+  // phase; the hardware interleaves one's MFMAs with the other's softmax.
   auto step = [&](auto S_, int t) {
     constexpr int S = decltype(S_)::value;
-    // M(t)
+    if (issuer && t + LEAD < ntiles) issue((S + LEAD) & 3, t + LEAD);
     const int ts = k0 + kPreKeys * t;
     const bool live = t < ntiles && ts < kend;
     f32x4 sc[NM][2];
@@ -1494,6 +1494,8 @@ __device__ __attribute__((always_inline)) inline void prefill_wg(const AttnArgs&
       if (live) {
         wa.qk_ops(kop[0], 0, sc);
         wa.qk_ops(kop[1], 1, sc);
+        wa.template read_vt<Tile>(slot(S) + Tile::BYTES, 0, va);
+        wa.softmax_tile(sl, sc, t >= nfull, ts, kend, pb);
       }
     } else {
       u32x4 kh[WA::NC];
@@ -1506,21 +1508,16 @@ __device__ __attribute__((always_inline)) inline void prefill_wg(const AttnArgs&
         wa.qk_ops(kh, 0, sc);
         wa.template k_operands<Tile>(slot(S), 1, kh);
         wa.qk_ops(kh, 1, sc);
+        wa.softmax_tile(sl, sc, t >= nfull, ts, kend, pb);
       }
     }
-    half_barrier();
-    // X(t): tiles t+1 .. t+LEAD-1 are in flight; tile t+1 lands before the
-    // barrier that precedes M(t+1).
+    pv_due = live;
     if (issuer && t + 1 < ntiles) {
-      if (LEAD > 2 && t + 2 < ntiles) wait_vmcnt<PER_TILE>();
+      // tiles t+1 .. min(t+LEAD, ntiles-1) are in flight: all but t+1 may stay
+      if (LEAD > 2 && t + 3 < ntiles) wait_vmcnt<2 * PER_TILE>();
+      else if (t + 2 < ntiles) wait_vmcnt<PER_TILE>();
       else wait_vmcnt<0>();
     }
-    if (issuer && t + LEAD < ntiles) issue((S + LEAD) & 3, t + LEAD);
-    if (live) {
-      if constexpr (kVAhead) wa.template read_vt<Tile>(slot(S) + Tile::BYTES, 0, va);
-      wa.softmax_tile(sl, sc, t >= nfull, ts, kend, pb);
-    }
-    pv_due = live;
     half_barrier();
   };
   for (int t = 0; t <= ntiles; t += 4) {
@@ -1532,7 +1529,6 @@ __device__ __attribute__((always_inline)) inline void prefill_wg(const AttnArgs&
     if (t + 3 > ntiles) break;
     step(std::integral_constant<int, 3>{}, t + 3);
   }
-  if (grp == 0) half_barrier();
   float ltot[NM];
   wa.row_sums(ltot);
 #pragma unroll
@@ -2019,7 +2015,14 @@ static bool plan_decode(const int32_t* q_lens, const int32_t* k_lens, const int3
   // `groups` work-groups.  Taken when the cut plan cut a segment and the
   // uncut one is within a merge launch of balanced, and when segments that
   // fold shared-prefix partials are in the plan and nothing was cut (its
-  // packing mixes kv heads; see kMixCandidates).
+  // packing mixes kv heads; see kMixCandidates).  On the 64-row GQA decode
+  // workload it leaves work-groups at 118-140 slices against an even 131, and
+  // no packing of whole segments does better there (best-fit decreasing under
+  // a cap and a simulated-annealing search over moves and swaps both stop at
+  // 140).  Measured and not kept: listing the fullest work-groups first (no
+  // change there, +14 us on the mixed batch), and idling waves of the lighter
+  // work-groups in proportion (no change: a CU's rate did not follow its
+  // waves in flight).
   bool any_cut = false, any_fold = false;
   for (size_t sg = 0; sg < seg_parts.size(); ++sg) {
     any_cut = any_cut || seg_parts[sg] > 1;

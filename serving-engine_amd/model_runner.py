@@ -43,44 +43,69 @@ class _PagedKVCache:
         self.kv_cache = kv_cache
         self.num_kv_heads = kv_cache.shape[-2]
         self.head_dim = kv_cache.shape[-1]
+        self._pool = None      # the pool's launch constants, for write()
+        self._strides = {}     # ctypes stride arrays of key/value layouts seen by write()
+
+    def _pool_args(self):
+        """(pool, base pointer, layer and K/V byte strides, block/token/head/dim
+        strides as a ctypes array, block size, blocks, dtype, dtype code,
+        device index), computed once per pool tensor."""
+        kv = self.kv_cache
+        pool = self._pool
+        if pool is None or pool[0] is not kv:
+            st, es = kv.stride(), kv.element_size()
+            pool = (kv, kv.data_ptr(), st[0] * es, st[1] * es, _lib.i64_array(st[2:]), kv.shape[3], kv.shape[2],
+                    kv.dtype, _lib.dtype_code(kv.dtype), kv.get_device())
+            self._pool = pool
+        return pool
+
+    def _stride_array(self, strides):
+        arr = self._strides.get(strides)
+        if arr is None:
+            if len(self._strides) > 64:
+                self._strides.clear()
+            arr = self._strides[strides] = _lib.i64_array(strides)
+        return arr
 
     def write(self, key_states, value_states, layer_idx, write_index):
         """Scatter new K/V into their slots: k_cache.view(-1, Hkv, D)[write_index[i]] =
         key_states[0, :, i, :] (serving_engine/model_runner.py:21-32), as one
         kvhot_reshape_and_cache launch for K and V.  key_states/value_states:
         [1, Hkv, S, D]; write_index: int64 (or int32) [S] on the cache device.
-        Slots outside the pool are skipped instead of raising."""
-        key = key_states.transpose(1, 2).squeeze(0)  # [S, Hkv, D] view, no copy
-        value = value_states.transpose(1, 2).squeeze(0)
-        k_cache = self.kv_cache[layer_idx, 0]
-        v_cache = self.kv_cache[layer_idx, 1]
-        if key.dim() != 3 or key.shape != value.shape:
+        Slots outside the pool are skipped instead of raising.  (The launch
+        reads the [S, Hkv, D] views' strides straight from the [1, Hkv, S, D]
+        tensors: an engine calls this once per layer per step.)"""
+        kv, base, layer_bytes, kv_bytes, cache_strides, bs, nblocks, dtype, code, dev = self._pool_args()
+        shape = key_states.shape
+        if len(shape) != 4 or shape[0] != 1 or value_states.shape != shape:
             raise ValueError(f"key {tuple(key_states.shape)} / value {tuple(value_states.shape)} must be [1, Hkv, S, D]")
-        s, hkv, d = key.shape
+        _, hkv, s, d = shape
         if hkv != self.num_kv_heads or d != self.head_dim:
             raise ValueError(f"key/value heads/dim {hkv}/{d} do not match the cache {self.num_kv_heads}/{self.head_dim}")
-        if key.dtype != k_cache.dtype or value.dtype != v_cache.dtype:
-            raise TypeError(f"key/value dtype {key.dtype} does not match the cache dtype {k_cache.dtype}")
+        if key_states.dtype != dtype or value_states.dtype != dtype:
+            raise TypeError(f"key/value dtype {key_states.dtype} does not match the cache dtype {dtype}")
         if write_index.dim() != 1 or write_index.shape[0] != s:
             raise ValueError(f"write_index must be [{s}], got {tuple(write_index.shape)}")
-        if write_index.dtype not in (torch.int64, torch.int32):
+        if write_index.dtype is not torch.int64 and write_index.dtype is not torch.int32:
             raise TypeError(f"write_index must be int64 or int32, got {write_index.dtype}")
-        dev = k_cache.device
-        if key.device != dev or value.device != dev or write_index.device != dev:
+        if key_states.get_device() != dev or value_states.get_device() != dev or write_index.get_device() != dev:
             raise ValueError("key, value, write_index and the cache must be on one GPU")
+        if not 0 <= layer_idx < kv.shape[0]:
+            raise IndexError(f"layer {layer_idx} outside the pool's {kv.shape[0]} layers")
         if s == 0:
             return
-        write_index = write_index.contiguous()
-        lib = _lib.load()
-        status = lib.kvhot_reshape_and_cache(
-            key.data_ptr(), _lib.i64_array(key.stride()),
-            value.data_ptr(), _lib.i64_array(value.stride()),
-            k_cache.data_ptr(), _lib.i64_array(k_cache.stride()),
-            v_cache.data_ptr(), _lib.i64_array(v_cache.stride()),
-            write_index.data_ptr(), 1 if write_index.dtype == torch.int64 else 0,
-            s, hkv, d, k_cache.shape[1], k_cache.shape[0],
-            _lib.dtype_code(k_cache.dtype), _lib.stream_handle(dev))
-        _lib.check(status, "kvhot_reshape_and_cache")
+        if not write_index.is_contiguous():
+            write_index = write_index.contiguous()
+        ks, vs = key_states.stride(), value_states.stride()
+        k_cache = base + layer_idx * layer_bytes
+        status = _lib.load().kvhot_reshape_and_cache(
+            key_states.data_ptr(), self._stride_array((ks[2], ks[1], ks[3])),
+            value_states.data_ptr(), self._stride_array((vs[2], vs[1], vs[3])),
+            k_cache, cache_strides, k_cache + kv_bytes, cache_strides,
+            write_index.data_ptr(), 1 if write_index.dtype is torch.int64 else 0,
+            s, hkv, d, bs, nblocks, code, _lib.stream_handle(kv.device))
+        if status:
+            _lib.check(status, "kvhot_reshape_and_cache")
 
     def update(self, key_states, value_states, layer_idx, read_index, write_index):
         """Eager path: write, then gather a dense [len(read_index), Hkv, D]
