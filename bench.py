@@ -63,6 +63,7 @@ Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload 2]
        python bench.py --copy-probe      # kvhot_copy_blocks of 256 MiB each way
                                          # (counter calibration)
        python bench.py --prefill-only    # the prefill measurement alone
+       python bench.py --legs-only       # the append_large, prefix and long_context legs alone
        python bench.py --copy-only       # the copy-on-write block copy alone
 """
 from __future__ import annotations
@@ -110,6 +111,8 @@ def parse():
                     help="only the prefill measurement (for counter runs); prints its JSON object")
     ap.add_argument("--no-legs", action="store_true",
                     help="skip the append_large, prefix and long_context legs")
+    ap.add_argument("--legs-only", action="store_true",
+                    help="only the append_large, prefix and long_context legs; prints their JSON objects")
     ap.add_argument("--no-engine", action="store_true", help="skip the engine tokens/s measurement")
     ap.add_argument("--no-copy", action="store_true", help="skip the copy-on-write block copy measurement")
     ap.add_argument("--copy-only", action="store_true",
@@ -137,11 +140,18 @@ def launch_list_desc(meta, w):
     parts = []
     if n_pfx:
         parts.append(f"attn_prefill_kernel<{tt},{w.head_dim}> x {n_pfx} shared-prefix units")
-    parts.append(f"attn_decode_kernel<{tt},{w.head_dim}> x {n_dec} waves")
+    n_chunk = n_pre - n_pfx
+    if n_chunk and n_dec and w.head_dim <= 128:
+        # the library fuses the two into one launch when a decode work-group's
+        # slots fit beside the prefill ring in one CU's LDS (head_dim <= 128)
+        parts.append(f"attn_mixed_kernel<{tt},{w.head_dim}> x ({n_chunk} prefill units + {n_dec} decode waves)")
+    else:
+        if n_chunk:
+            parts.append(f"attn_prefill_kernel<{tt},{w.head_dim}> x {n_chunk} units")
+        if n_dec:
+            parts.append(f"attn_decode_kernel<{tt},{w.head_dim}> x {n_dec} waves")
     if n_mrg:
         parts.append(f"attn_merge_kernel<{tt},{w.head_dim}> x {n_mrg} units")
-    if n_pre > n_pfx:
-        parts.append(f"attn_prefill_kernel<{tt},{w.head_dim}> x {n_pre - n_pfx} units on a second stream")
     return "one attention call: " + " + ".join(parts)
 
 
@@ -267,6 +277,19 @@ def main():
         sea = importlib.import_module("serving-engine_amd")
         wl = importlib.import_module("serving-engine_amd.workloads")
         print(json.dumps({"copy": copy_measure(sea, wl, torch.device("cuda:0"), reps=max(1, args.kernel_reps))}),
+              flush=True)
+        return
+    if args.legs_only:
+        import torch
+
+        torch.cuda.set_device(0)
+        sea = importlib.import_module("serving-engine_amd")
+        wl = importlib.import_module("serving-engine_amd.workloads")
+        dev = torch.device("cuda:0")
+        reps = max(1, args.kernel_reps)
+        print(json.dumps({"append_large": append_leg(sea, wl, dev, reps),
+                          "prefix": attention_leg(sea, wl, dev, 4, layers=16, reps=reps),
+                          "long_context": attention_leg(sea, wl, dev, 5, layers=1, reps=max(3, reps // 2), calls=8)}),
               flush=True)
         return
     if args.prefill_only:
