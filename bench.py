@@ -140,16 +140,10 @@ def launch_list_desc(meta, w):
     parts = []
     if n_pfx:
         parts.append(f"attn_prefill_kernel<{tt},{w.head_dim}> x {n_pfx} shared-prefix units")
-    n_chunk = n_pre - n_pfx
-    if n_chunk and n_dec and w.head_dim <= 128:
-        # the library fuses the two into one launch when a decode work-group's
-        # slots fit beside the prefill ring in one CU's LDS (head_dim <= 128)
-        parts.append(f"attn_mixed_kernel<{tt},{w.head_dim}> x ({n_chunk} prefill units + {n_dec} decode waves)")
-    else:
-        if n_chunk:
-            parts.append(f"attn_prefill_kernel<{tt},{w.head_dim}> x {n_chunk} units")
-        if n_dec:
-            parts.append(f"attn_decode_kernel<{tt},{w.head_dim}> x {n_dec} waves")
+    if n_pre > n_pfx:
+        parts.append(f"attn_prefill_kernel<{tt},{w.head_dim}> x {n_pre - n_pfx} units")
+    if n_dec:
+        parts.append(f"attn_decode_kernel<{tt},{w.head_dim}> x {n_dec} waves")
     if n_mrg:
         parts.append(f"attn_merge_kernel<{tt},{w.head_dim}> x {n_mrg} units")
     return "one attention call: " + " + ".join(parts)
@@ -811,7 +805,7 @@ def prefill_measure(sea, wl, dev, reps, layers=16):
     tflops = flops / (out["prefill_rows"] * 1e-6) / 1e12
     return {
         "workload": full.name,
-        "kernel": "attn_prefill_kernel<BF16,128,2> (8 prefill rows only)",
+        "kernel": "attn_prefill_kernel<BF16,128,2> (8 prefill rows only; 4-wave work-groups, two per CU)",
         "bound": "mfma",
         "flops_per_call": flops,
         "avg_call_us": round(out["prefill_rows"], 3),

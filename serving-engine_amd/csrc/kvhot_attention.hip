@@ -225,6 +225,7 @@ struct WaveAttn {
   bool mval[NM];
   u32x4 qf[NM][NC];  // Q as the B operand of S^T = K . Q^T
   float m[NM], l[NM];
+  float thr[NM];     // prefill tiles: raw score above which m[s] has to move
   f32x4 o[NM][EPL];  // O^T: lane (n, g) holds head_dim EPL*(4g+j)+e of m-row n
 
   // m-rows are the (query, head) pairs q0 + i / G, kvh * G + i % G of a row
@@ -407,15 +408,21 @@ struct WaveAttn {
       for (int s = 0; s < NM; ++s) sc[s][h] = TT::mfma(kop[c], qf[s][c], sc[s][h]);
   }
 
-  // Local (per-lane) max of each m-row's scores, in log2 units, and whether
-  // any exceeds its reference by more than kLazyRescale.
-  __device__ bool lazy_check(float sl, const f32x4 (&sc)[NM][2], float (&mloc)[NM]) const {
+  // Local (per-lane) max of each m-row's raw scores, and whether any exceeds
+  // its threshold thr[s] = (m[s] + kLazyRescale) / sl.  IEEE maximum (NaN in,
+  // NaN out) needs no canonicalising of the MFMA results and pairs into
+  // v_maximum3_f32: four instructions and one compare per m-row.  A NaN
+  // score leaves m alone and makes the row's P, and so its output, NaN.
+  __device__ static float max3(float x, float y, float z) {
+    return __builtin_elementwise_maximum(__builtin_elementwise_maximum(x, y), z);
+  }
+  __device__ bool lazy_check(const f32x4 (&sc)[NM][2], float (&mloc)[NM]) const {
     bool need = false;
 #pragma unroll
     for (int s = 0; s < NM; ++s) {
-      mloc[s] = fmaxf(fmaxf(fmaxf(sc[s][0][0], sc[s][0][1]), fmaxf(sc[s][0][2], sc[s][0][3])),
-                      fmaxf(fmaxf(sc[s][1][0], sc[s][1][1]), fmaxf(sc[s][1][2], sc[s][1][3]))) * sl;
-      need = need || mloc[s] > m[s] + kLazyRescale;
+      const f32x4 x = sc[s][0], y = sc[s][1];
+      mloc[s] = __builtin_elementwise_maximum(max3(x[3], y[0], y[1]), max3(y[2], y[3], max3(x[0], x[1], x[2])));
+      need = need || mloc[s] > thr[s];
     }
     return need;
   }
@@ -522,14 +529,15 @@ struct WaveAttn {
           }
     }
     float mloc[NM];
-    if (__builtin_amdgcn_ballot_w64(lazy_check(sl, sc, mloc)) != 0) {
+    if (__builtin_amdgcn_ballot_w64(lazy_check(sc, mloc)) != 0) {
 #pragma unroll
       for (int s = 0; s < NM; ++s) {
         float mx = fmaxf(mloc[s], __shfl_xor(mloc[s], 16, kWave));
-        mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+        mx = fmaxf(mx, __shfl_xor(mx, 32, kWave)) * sl;
         const float mnew = fmaxf(m[s], mx);
         const float corr = fast_exp2(m[s] - mnew);
         m[s] = mnew;
+        thr[s] = (mnew + kLazyRescale) / sl;
         l[s] *= corr;
 #pragma unroll
         for (int e = 0; e < EPL; ++e) o[s][e] *= corr;
@@ -1197,18 +1205,25 @@ attn_merge_kernel(const AttnArgs a) {
 }
 
 // -------------------------------------------------------------- prefill --
-// A work-group of kPreWaves waves takes consecutive query blocks of one
-// (row, kv head): wave w the 16*NM/G queries q0 + w*16*NM/G ... (all G heads of
-// each).  Keys are walked in 32-key tiles that the work-group copies from the
-// paged cache straight into LDS (buffer_load ... lds, no register staging)
-// through a ring of four slots, three tiles ahead of the one being computed,
-// so each K/V byte is read from HBM once per work-group and from LDS once per
-// wave.  A wave skips tiles wholly past its own causal limit.
-#ifndef KVHOT_PRE_WAVES
-#define KVHOT_PRE_WAVES 8
-#endif
-constexpr int kPreWaves = KVHOT_PRE_WAVES;  // 8: two per SIMD
-constexpr int kPreIssuers = 4;              // the leading wave of each SIMD
+// A work-group of prefill_waves(D) waves takes consecutive query blocks of
+// one (row, kv head): wave w the 16*NM/G queries q0 + w*16*NM/G ... (all G
+// heads of each).  Keys are walked in 32-key tiles that the work-group copies
+// from the paged cache straight into LDS (buffer_load ... lds, no register
+// staging) through a ring of four slots, three tiles ahead of the one being
+// computed, so each K/V byte is read from HBM once per work-group and from
+// LDS once per wave.  A wave skips tiles wholly past its own causal limit.
+//
+// At head_dim 64 and 128 a work-group is 4 waves, one per SIMD, and two
+// work-groups share a CU (64 KiB of ring each, at most 256 VGPRs a wave).
+// Their barriers are their own, so the two waves of a SIMD drift apart and
+// one's MFMAs run while the other forms its softmax; with one 8-wave
+// work-group per CU the two waves of a SIMD meet at every tile's barrier and
+// their softmax phases coincide (measured on the mixed workload's prefill
+// rows: 158 us with two 4-wave work-groups per CU against 172 us with one
+// 8-wave work-group).  At head_dim 256 (a 128 KiB ring) one 8-wave
+// work-group takes the CU.
+constexpr int prefill_waves(int64_t D) { return D == 256 ? 8 : 4; }
+constexpr int kPreIssuers = 4;  // waves 0-3 issue the DMA, one per SIMD
 constexpr int kPreKeys = 32;
 constexpr int kPreSlots = 4;
 
@@ -1266,6 +1281,7 @@ __device__ __attribute__((always_inline)) inline void prefill_wg(const AttnArgs&
   (void)by;
   using Tile = PreTile<D>;
   using WA = WaveAttn<TT, D, NM>;
+  constexpr int PW = prefill_waves(D);
   // Ring slots, K tile then V tile.  Separate arrays: the compiler can tell
   // that reads of one slot do not alias the DMA into another, and so does
   // not wait for every DMA in flight before each LDS read.
@@ -1307,7 +1323,7 @@ __device__ __attribute__((always_inline)) inline void prefill_wg(const AttnArgs&
       k0 = u.z;
       kend_g = u.w;
       qs = u1.x;
-      nqg = min(u1.y, QPW * kPreWaves);
+      nqg = min(u1.y, QPW * PW);
       pbase = u1.z;
       pstride = u1.w;
     } else {
@@ -1336,9 +1352,9 @@ __device__ __attribute__((always_inline)) inline void prefill_wg(const AttnArgs&
   } else {
     const int qlen = a.q_lens[row];
     if (qlen < 2) return;
-    q0g = qblk * QPW * kPreWaves;
+    q0g = qblk * QPW * PW;
     if (q0g >= qlen) return;
-    nqg = min(QPW * kPreWaves, qlen - q0g);
+    nqg = min(QPW * PW, qlen - q0g);
     off = a.q_offs[row];
     const int klen = a.k_lens[row];
     kend_g = max(a.causal ? min(klen, off + q0g + nqg) : klen, 0);
@@ -1456,7 +1472,10 @@ __device__ __attribute__((always_inline)) inline void prefill_wg(const AttnArgs&
   }
   sl = fmaxf(sl, 1e-30f);
 #pragma unroll
-  for (int s = 0; s < NM; ++s) wa.m[s] = -FLT_MAX;
+  for (int s = 0; s < NM; ++s) {
+    wa.m[s] = -FLT_MAX;
+    wa.thr[s] = -INFINITY;  // the first visible score moves m
+  }
   half_barrier();
 
   // A phase issues all of tile t's K reads first and runs PV(t-1) from
@@ -1542,30 +1561,11 @@ __device__ __attribute__((always_inline)) inline void prefill_wg(const AttnArgs&
   }
 }
 
+// Two waves per SIMD at every head_dim (at most 256 VGPRs a wave).
 template <class TT, int D, int NM>
-__global__ void __launch_bounds__(64 * kPreWaves)
+__global__ void __launch_bounds__(64 * prefill_waves(D)) __attribute__((amdgpu_waves_per_eu(2)))
 attn_prefill_kernel(const AttnArgs a) {
   prefill_wg<TT, D, NM>(a, a.sched, blockIdx.x, blockIdx.y, blockIdx.z);
-}
-
-// ---------------------------------------------------------------- mixed --
-// A batch of prefill and decode rows in one launch: work-groups [0, n_pre)
-// are prefill units (longest first), the rest decode work-groups.  Work-groups
-// are dispatched in order, so every prefill unit starts before any decode
-// work-group, and the decode work-groups take the CUs the prefill tail leaves
-// idle.  (Two launches leave those CUs idle; two streams let decode
-// work-groups interleave with the prefill units and put their longest-first
-// order off.)  Both bodies run 8-wave work-groups; the launch holds the
-// prefill's static LDS ring and the decode's dynamic LDS.
-template <class TT, int D, int NM, int W>
-__global__ void __launch_bounds__(64 * kPreWaves)
-attn_mixed_kernel(const AttnArgs a, const int4* pre_units, int n_pre) {
-  static_assert(W == kPreWaves, "one work-group size for both bodies");
-  const int b = blockIdx.x;
-  if (b < n_pre)
-    prefill_wg<TT, D, NM>(a, pre_units, b, 0, 0);
-  else
-    decode_wg<TT, D, W>(a, a.sched, b - n_pre, 0, 0);
 }
 
 // ----------------------------------------------------------- VALU kernel --
@@ -1687,25 +1687,16 @@ static int64_t decode_lds_limit(int W, int64_t G, int64_t D) {
   return decode_lds_words(W, W, G, D) * 4 <= kMaxLdsBytes ? kMaxLdsBytes : kCuLdsBytes;
 }
 
-// LDS slots of a decode work-group of W waves in `limit` bytes of LDS: one per
-// wave plus a pool of up to W more for waves that move on to other segments,
-// as LDS allows; 0 when one slot per wave does not fit.
-static int decode_slots_within(int W, int64_t G, int64_t D, int64_t limit) {
+// LDS slots of a decode work-group of W waves: one per wave plus a pool of up
+// to W more for waves that move on to other segments, as LDS allows; 0 when
+// one slot per wave does not fit.
+static int decode_slots(int W, int64_t G, int64_t D) {
+  const int64_t limit = decode_lds_limit(W, G, D);
   const int64_t base = decode_lds_words(W, W, G, D);
   if (base * 4 > limit) return 0;
   const int64_t spare = limit / 4 - base;
   const int64_t per_slot = G * D + G + 4;
   return W + static_cast<int>(std::max<int64_t>(0, std::min<int64_t>(W, spare / per_slot)));
-}
-
-static int decode_slots(int W, int64_t G, int64_t D) {
-  return decode_slots_within(W, G, D, decode_lds_limit(W, G, D));
-}
-
-// Static LDS of a prefill work-group: the four-slot ring of K and V tiles.
-template <int D>
-constexpr int64_t prefill_ring_bytes() {
-  return static_cast<int64_t>(kPreSlots) * 2 * PreTile<D>::BYTES;
 }
 
 // Bytes of one split-K partial: the normalised O and LSE of G query heads.
@@ -2182,7 +2173,7 @@ static void plan_prefill(const int32_t* q_lens, const int32_t* k_lens, const int
   for (int64_t r = 0; r < rows; ++r) {
     const int64_t qlen = q_lens[r], klen = k_lens[r], off = q_offs[r];
     if (qlen < 2) continue;
-    const int64_t qpw = kPreWaves * 16 * prefill_nm(D) / G;  // queries per work-group
+    const int64_t qpw = prefill_waves(D) * 16 * prefill_nm(D) / G;  // queries per work-group
     for (int64_t qb = 0; qb * qpw < qlen; ++qb) {
       const int64_t q0 = qb * qpw, nq = std::min(qpw, qlen - q0);
       const int64_t kend = std::max<int64_t>(causal ? std::min(klen, off + q0 + nq) : klen, 0);
@@ -2226,38 +2217,25 @@ static void launch_mfma(const AttnArgs& a, int waves, int64_t rows, int64_t max_
     // partials they write.
     AttnArgs xa = a;
     xa.sched = a.sched + 2 * n_dec;
-    hipLaunchKernelGGL((attn_prefill_kernel<TT, D, NM>), dim3(static_cast<uint32_t>(n_pfx)), dim3(64 * kPreWaves), 0,
+    hipLaunchKernelGGL((attn_prefill_kernel<TT, D, NM>), dim3(static_cast<uint32_t>(n_pfx)), dim3(64 * prefill_waves(D)), 0,
                        stream, xa);
   }
-  bool dec = !a.sched || n_dec > 0;
-  bool pre = a.sched ? n_pre > n_pfx : max_q >= 2;
-  if constexpr (D <= 128) {
-    // Prefill units and decode work-groups in one grid, when the prefill's
-    // LDS ring and a decode work-group's slots fit one CU's LDS together
-    // (never at head_dim 256, whose ring alone takes 128 KiB).
-    const int slots = decode_slots_within(waves, a.G, D, kCuLdsBytes - prefill_ring_bytes<D>());
-    if (dec && pre && a.sched && waves == kPreWaves && slots > 0) {
-      AttnArgs ma = a;
-      ma.dec_slots = slots;
-      const size_t lds = static_cast<size_t>(decode_lds_words(waves, slots, a.G, D) * 4);
-      auto* kern = &attn_mixed_kernel<TT, D, NM, kPreWaves>;
-      if (static_cast<int64_t>(lds) + prefill_ring_bytes<D>() > kMaxLdsBytes)
-        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                  static_cast<int>(lds));
-      const int64_t n_units = n_pre - n_pfx;
-      hipLaunchKernelGGL(kern, dim3(static_cast<uint32_t>(n_units + n_dec / waves)), dim3(64 * kPreWaves), lds, stream,
-                         ma, a.sched + 2 * (n_dec + n_pfx), static_cast<int>(n_units));
-      dec = pre = false;
-    }
-  }
+  // Prefill units, then the decode work-groups, in launch order on the
+  // caller's stream.  (One launch holding both -- prefill units first,
+  // decode work-groups taking the CUs the prefill tail leaves idle -- needs
+  // one work-group size for both; with 8-wave prefill work-groups it saved
+  // 6 us on the mixed workload, less than two 4-wave prefill work-groups per
+  // CU save in the prefill alone.)
+  const bool dec = !a.sched || n_dec > 0;
+  const bool pre = a.sched ? n_pre > n_pfx : max_q >= 2;
   if (pre) {
-    const int64_t qpw = kPreWaves * 16 * NM / a.G;
+    const int64_t qpw = prefill_waves(D) * 16 * NM / a.G;
     const int64_t nqb = (max_q + qpw - 1) / qpw;
     dim3 grid = a.sched ? dim3(static_cast<uint32_t>(n_pre - n_pfx))
                         : dim3(static_cast<uint32_t>(a.Hkv * nqb), 1u, static_cast<uint32_t>(rows));
     AttnArgs pa = a;
     if (a.sched) pa.sched = a.sched + 2 * (n_dec + n_pfx);
-    hipLaunchKernelGGL((attn_prefill_kernel<TT, D, NM>), grid, dim3(64 * kPreWaves), 0, stream, pa);
+    hipLaunchKernelGGL((attn_prefill_kernel<TT, D, NM>), grid, dim3(64 * prefill_waves(D)), 0, stream, pa);
   }
   if (dec) {
     bool launched = false;
@@ -2333,7 +2311,7 @@ extern "C" int64_t kvhot_paged_attention_schedule(
   if (pl.mfma) {
     const int64_t G = num_q_heads / num_kv_heads;
     const int64_t groups = resident_decode_waves(dtype, head_dim, pl.waves, G) / pl.waves;
-    const int64_t prefix_queries = kPreWaves * 16 * prefill_nm(head_dim) / G;  // per prefill work-group
+    const int64_t prefix_queries = prefill_waves(head_dim) * 16 * prefill_nm(head_dim) / G;  // per prefill work-group
     if (plan_decode(q_lens, k_lens, q_pos_offsets, q_starts, block_table, bt_row_stride, block_size,
                     num_rows, num_kv_heads, is_causal, pl.waves, groups, partition_tokens,
                     32 * head_dim * dtype_size(dtype), prefix_queries, dec, mrg, pfx, partials)) {

@@ -281,7 +281,7 @@ def test_schedule_lists_every_unit_once(lib):
     _check_decode_schedule(dec, merge, ws, qs, W, {0: 300, 1: 40, 4: 2000}, 8, pt=1024)
     # the 2000-key row has two 1024-key partitions per kv head, the others one
     assert sorted(merge[:, 2].tolist()) == [2] * 8
-    # prefill: 20 queries, 64 per work-group (4 waves x 64 m-rows / G=4) -> 1 block x 8 kv heads;
+    # prefill: 20 queries, 32 per work-group at head_dim 128 (4 waves x 32 m-rows / G=4) -> 1 block x 8 kv heads;
     # the empty chunk has none
     assert sorted(map(tuple, pre[:, :3].tolist())) == sorted((2, h, 0) for h in range(8))
     # the block's last query (position 49) sees 50 keys: two 32-key tiles
@@ -290,14 +290,16 @@ def test_schedule_lists_every_unit_once(lib):
 
 
 def test_schedule_prefill_blocks_longest_first(lib):
-    """Prefill work-groups take 64 queries (G=4) and are listed by key tiles, most first."""
+    """Prefill work-groups take 32 queries at head_dim 128 (4 waves x 32
+    m-rows / G=4) and are listed by key tiles, most first."""
     # one 150-query chunk at positions 100..249 (250 keys), one 40-query chunk on 40 keys
     dec, pre, merge, ws, qs = _schedule(lib, [150, 40], [250, 40], [100, 0])
     assert len(dec) == 0 and len(merge) == 0
     units = sorted(map(tuple, pre[:, :4].tolist()))
-    # row 0: blocks of queries 0-63, 64-127, 128-149 -> visible keys 164, 228, 250 -> 6, 8, 8 tiles
-    want = [(0, h, b, t) for h in range(8) for b, t in ((0, 6), (1, 8), (2, 8))]
-    want += [(1, h, 0, 2) for h in range(8)]
+    # row 0: blocks of queries 0-31, ..., 128-149 -> visible keys 132, 164, 196, 228, 250 -> 5, 6, 7, 8, 8 tiles
+    want = [(0, h, b, t) for h in range(8) for b, t in ((0, 5), (1, 6), (2, 7), (3, 8), (4, 8))]
+    # row 1: queries 0-31 see 32 keys (1 tile), 32-39 see 40 (2 tiles)
+    want += [(1, h, b, t) for h in range(8) for b, t in ((0, 1), (1, 2))]
     assert units == sorted(want)
     assert list(pre[:, 3]) == sorted(pre[:, 3], reverse=True)
 
@@ -457,7 +459,8 @@ def test_schedule_shared_prefix_units(lib):
     import numpy as np
 
     hq, hkv, d, G = 32, 8, 128, 4
-    pq = 8 * 16 * 2 // G  # queries per prefix unit at D=128: 64
+    pq = 4 * 16 * 2 // G  # queries per prefix unit at D=128 (4 waves x 32 m-rows / G): 32
+    nqb = -(-70 // pq)
     q_lens = [40] + [1] * 70 + [1] * 2 + [1] * 3
     k_lens = [100] + [1500 + 37 * i for i in range(70)] + [900, 2100] + [800, 810, 820]
     offs = [60] + [k - 1 for k in k_lens[1:]]
@@ -467,8 +470,8 @@ def test_schedule_shared_prefix_units(lib):
     bt[1:71, :70] = 500000 + np.arange(70)  # 70 shared blocks: 1120 keys
     bt[73:76, :40] = 600000 + np.arange(40)  # only three rows: no group
     dec, pre, merge, ws, qs, npx = _schedule(lib, q_lens, k_lens, offs, hq=hq, hkv=hkv, d=d, bt=bt, prefix=True)
-    assert npx > 0 and npx % (2 * hkv) == 0  # two query blocks of the 70 rows, every kv head
-    ks = npx // (2 * hkv)
+    assert npx > 0 and npx % (nqb * hkv) == 0  # every query block of the 70 rows, every kv head
+    ks = npx // (nqb * hkv)
     assert 1 <= ks <= 1120 // 128
     pb = G * (d + 1) * 4
     nparts_total = ws // pb
@@ -477,8 +480,8 @@ def test_schedule_shared_prefix_units(lib):
     assert len(pidx_of) == 70 * hkv
     # prefix units: (row, kv head, k0, k1), (query token, queries, partial, stride)
     pfx = pre[:npx].reshape(-1, 2, 4)
-    rest = pre[npx:].reshape(-1, 2, 4)  # the prefill row's units follow
-    assert len(rest) == hkv and all(u[0][0] == 0 and not u[1].any() for u in rest)
+    rest = pre[npx:].reshape(-1, 2, 4)  # the prefill row's units follow: its 40 queries in two blocks
+    assert len(rest) == 2 * hkv and all(u[0][0] == 0 and not u[1].any() for u in rest)
     tiles = {}
     written = []
     for (r0, h, k0, k1), (qtok, nq, base, stride) in pfx.tolist():
