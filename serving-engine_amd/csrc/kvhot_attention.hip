@@ -428,10 +428,8 @@ struct WaveAttn {
   }
 
   // P = 2^(S sl - m) as the packed B operand of the PV product, and this
-  // lane's row sums.  Returns whether some P exceeds 2^kLazyRescale (a score
-  // more than kLazyRescale above its reference, which the fast path may not
-  // take); the test reads P, so P is formed before any branch on it.
-  __device__ void probs(float sl, const f32x4 (&sc)[NM][2], u32x4 (&pb)[NM]) {
+  // lane's sums of P per m-row (ls, not yet added to l).
+  __device__ void probs(float sl, const f32x4 (&sc)[NM][2], u32x4 (&pb)[NM], float (&ls)[NM]) const {
 #pragma unroll
     for (int s = 0; s < NM; ++s) {
       float p[2][4];
@@ -439,10 +437,44 @@ struct WaveAttn {
       for (int h = 0; h < 2; ++h)
 #pragma unroll
         for (int j = 0; j < 4; ++j) p[h][j] = fast_exp2(__builtin_fmaf(sc[s][h][j], sl, -m[s]));
-      l[s] += ((p[0][0] + p[0][1]) + (p[0][2] + p[0][3])) + ((p[1][0] + p[1][1]) + (p[1][2] + p[1][3]));
+      ls[s] = ((p[0][0] + p[0][1]) + (p[0][2] + p[0][3])) + ((p[1][0] + p[1][1]) + (p[1][2] + p[1][3]));
       pb[s] = u32x4{TT::pack2(p[0][0], p[0][1]), TT::pack2(p[0][2], p[0][3]),
                     TT::pack2(p[1][0], p[1][1]), TT::pack2(p[1][2], p[1][3])};
     }
+  }
+
+  // Moves the references of the m-rows whose scores call for it (mloc: this
+  // lane's raw maxima from lazy_check): the new reference is the row's
+  // maximum in log2 units, O and the row sums are rescaled to it.
+  __device__ void move_refs(float sl, const float (&mloc)[NM]) {
+#pragma unroll
+    for (int s = 0; s < NM; ++s) {
+      float mx = fmaxf(mloc[s], __shfl_xor(mloc[s], 16, kWave));
+      mx = fmaxf(mx, __shfl_xor(mx, 32, kWave)) * sl;
+      const float mnew = fmaxf(m[s], mx);
+      const float corr = fast_exp2(m[s] - mnew);
+      m[s] = mnew;
+      thr[s] = (mnew + kLazyRescale) / sl;
+      l[s] *= corr;
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) o[s][e] *= corr;
+    }
+  }
+
+  // Softmax of a tile with no masked key: P formed with the current
+  // references first, so that everything up to the rare move of a
+  // reference is one branch-free block the scheduler can interleave with
+  // MFMAs, and formed again after a move.
+  __device__ void softmax_nomask(float sl, const f32x4 (&sc)[NM][2], u32x4 (&pb)[NM]) {
+    float mloc[NM], ls[NM];
+    const bool need = lazy_check(sc, mloc);
+    probs(sl, sc, pb, ls);
+    if (__builtin_amdgcn_ballot_w64(need) != 0) {
+      move_refs(sl, mloc);
+      probs(sl, sc, pb, ls);
+    }
+#pragma unroll
+    for (int s = 0; s < NM; ++s) l[s] += ls[s];
   }
 
   // V^T operands of a tile, read with ds_read_b64_tr_b16.  Within a 16-lane
@@ -516,34 +548,24 @@ struct WaveAttn {
   // or past an m-row's causal limit masked when `mask`, references moved and
   // O and the row sums rescaled when a score calls for it, row sums added;
   // P packed as the B operand of the tile's PV product.
+  __device__ void mask_tile(f32x4 (&sc)[NM][2], int ts, int kstop) const {
+#pragma unroll
+    for (int s = 0; s < NM; ++s)
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int tk = ts + 16 * h + 4 * g + j;
+          sc[s][h][j] = (tk < kstop && tk <= qlimit(s)) ? sc[s][h][j] : -INFINITY;
+        }
+  }
   __device__ void softmax_tile(float sl, f32x4 (&sc)[NM][2], bool mask, int ts, int kstop, u32x4 (&pb)[NM]) {
-    if (mask) {
+    if (mask) mask_tile(sc, ts, kstop);
+    float mloc[NM], ls[NM];
+    if (__builtin_amdgcn_ballot_w64(lazy_check(sc, mloc)) != 0) move_refs(sl, mloc);
+    probs(sl, sc, pb, ls);
 #pragma unroll
-      for (int s = 0; s < NM; ++s)
-#pragma unroll
-        for (int h = 0; h < 2; ++h)
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const int tk = ts + 16 * h + 4 * g + j;
-            sc[s][h][j] = (tk < kstop && tk <= qlimit(s)) ? sc[s][h][j] : -INFINITY;
-          }
-    }
-    float mloc[NM];
-    if (__builtin_amdgcn_ballot_w64(lazy_check(sc, mloc)) != 0) {
-#pragma unroll
-      for (int s = 0; s < NM; ++s) {
-        float mx = fmaxf(mloc[s], __shfl_xor(mloc[s], 16, kWave));
-        mx = fmaxf(mx, __shfl_xor(mx, 32, kWave)) * sl;
-        const float mnew = fmaxf(m[s], mx);
-        const float corr = fast_exp2(m[s] - mnew);
-        m[s] = mnew;
-        thr[s] = (mnew + kLazyRescale) / sl;
-        l[s] *= corr;
-#pragma unroll
-        for (int e = 0; e < EPL; ++e) o[s][e] *= corr;
-      }
-    }
-    probs(sl, sc, pb);
+    for (int s = 0; s < NM; ++s) l[s] += ls[s];
   }
 
   // Row sums over the four lane groups that share an m-row.
@@ -1225,6 +1247,17 @@ attn_merge_kernel(const AttnArgs a) {
 constexpr int prefill_waves(int64_t D) { return D == 256 ? 8 : 4; }
 constexpr int kPreIssuers = 4;  // waves 0-3 issue the DMA, one per SIMD
 constexpr int kPreKeys = 32;
+// Interleave of the pipelined prefill phase: softmax VALU instructions
+// before the first QK MFMA, and after each QK MFMA.
+#ifndef KVHOT_PRE_SCHED
+#define KVHOT_PRE_SCHED 1
+#endif
+#ifndef KVHOT_PRE_VALU_LEAD
+#define KVHOT_PRE_VALU_LEAD 8
+#endif
+#ifndef KVHOT_PRE_VALU_PER_MFMA
+#define KVHOT_PRE_VALU_PER_MFMA 4
+#endif
 constexpr int kPreSlots = 4;
 
 // A K (or V) tile in LDS: 32 key rows of 2*D bytes.  The 16-byte chunks of a
@@ -1478,45 +1511,122 @@ __device__ __attribute__((always_inline)) inline void prefill_wg(const AttnArgs&
   }
   half_barrier();
 
-  // A phase issues all of tile t's K reads first and runs PV(t-1) from
-  // registers while they land, and reads tile t's V^T operands for PV(t) in
-  // the next phase.  D = 256 (registers): K half a tile at a time, and tile
-  // t-1's V^T read in phase t itself.
   constexpr bool kVAhead = WA::NC <= 4;
-  u32x4 pb[NM];           // P of the previous tile, for its PV
-  u32x4 va[WA::VB];       // its V^T operands
-  bool pv_due = false;    // the previous tile had keys this wave sees
-  // One phase per tile, ending in the tile's one barrier.  At its start the
-  // issuing waves put tile t+LEAD in flight, into the slot of tile t+LEAD-4:
-  // at LEAD 3 tile t-1's, whose K and V^T reads ended before the last
-  // barrier (PV(t-1) runs from registers); at LEAD 2 (D = 256, V^T read for
-  // PV(t-1) in this phase) tile t-2's.  Each wave then reads tile t's K, runs
-  // PV(t-1), QK(t), reads tile t's V^T and forms P(t).  Before the barrier an
-  // issuing wave waits for its part of tile t+1: its DMAs complete in issue
-  // order, and the only vector memory operations in the loop are these DMAs,
-  // so vmcnt <= (tiles in flight after t+1) * PER_TILE means tile t+1's
-  // PER_TILE instructions have landed.  The two waves of a SIMD run the same
-  // phase; the hardware interleaves one's MFMAs with the other's softmax.
-  auto step = [&](auto S_, int t) {
-    constexpr int S = decltype(S_)::value;
-    if (issuer && t + LEAD < ntiles) issue((S + LEAD) & 3, t + LEAD);
-    const int ts = k0 + kPreKeys * t;
-    const bool live = t < ntiles && ts < kend;
-    f32x4 sc[NM][2];
-    if constexpr (kVAhead) {
+  if constexpr (kVAhead) {
+    // head_dim 64 and 128, software-pipelined: phase t reads K(t+1) and
+    // V^T(t), runs QK(t+1) while it forms P(t) from the scores QK(t) left in
+    // scc one phase earlier, then PV(t).  The QK MFMAs and the softmax VALU
+    // of one wave are independent, so they interleave (sched_group_barrier
+    // below) instead of the softmax waiting for the QK results.  At its start
+    // the issuing waves put tile t+3 in flight into the slot of tile t-1
+    // (its K read in phase t-2, its V^T in phase t-1, both before the last
+    // barrier); before the barrier an issuing wave waits for its part of
+    // tile t+2, whose K phase t+1 reads: its DMAs complete in issue order,
+    // and the only vector memory operations in the loop are these DMAs, so
+    // vmcnt <= PER_TILE (tile t+3 alone still in flight) or 0 means tile
+    // t+2's PER_TILE instructions have landed.
+    f32x4 scc[NM][2];  // raw S of tile t
+    if (ntiles > 0) {
       u32x4 kop[2][WA::NC];
-      if (live) {
-        wa.template k_operands<Tile>(slot(S), 0, kop[0]);
-        wa.template k_operands<Tile>(slot(S), 1, kop[1]);
+      wa.template k_operands<Tile>(slot(0), 0, kop[0]);
+      wa.template k_operands<Tile>(slot(0), 1, kop[1]);
+      wa.qk_ops(kop[0], 0, scc);
+      wa.qk_ops(kop[1], 1, scc);
+    }
+    // Every wave runs every tile of the unit: a tile wholly past a wave's
+    // causal limit is masked like the diagonal one (P = 0), which keeps the
+    // phase one straight block.  Such tiles are at most one per wave, the
+    // waves of a work-group being 16*NM/G queries apart.
+    auto phase = [&](auto S_, int t) {
+      constexpr int S = decltype(S_)::value;
+      if (issuer && t + LEAD < ntiles) issue((S + LEAD) & 3, t + LEAD);
+      const int ts = k0 + kPreKeys * t;
+      if (t >= nfull) wa.mask_tile(scc, ts, kend);
+      const char* vt = slot(S) + Tile::BYTES;
+      const char* kn = slot((S + 1) & 3);
+      u32x4 va[WA::VB];
+      u32x4 pb[NM];
+      f32x4 scn[NM][2];
+      // References first (rare move, before the block), then one block:
+      // K(t+1) and V^T(t) reads, QK(t+1) and P(t).
+      float mloc[NM], ls[NM];
+      if (__builtin_amdgcn_ballot_w64(wa.lazy_check(scc, mloc)) != 0) wa.move_refs(sl, mloc);
+      u32x4 kop[2][WA::NC];
+      wa.template k_operands<Tile>(kn, 0, kop[0]);
+      wa.template k_operands<Tile>(kn, 1, kop[1]);
+      wa.template read_vt<Tile>(vt, 0, va);
+      wa.qk_ops(kop[0], 0, scn);
+      wa.qk_ops(kop[1], 1, scn);
+      wa.probs(sl, scc, pb, ls);
+#if KVHOT_PRE_SCHED
+      // The LDS reads first, then each QK MFMA followed by a few softmax
+      // VALU instructions.
+      __builtin_amdgcn_sched_group_barrier(0x100, 2 * WA::NC, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, KVHOT_PRE_VALU_LEAD, 0);
+#pragma unroll
+      for (int i = 0; i < 4 * NM * WA::NC; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        if (i < 2 * WA::VB) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, KVHOT_PRE_VALU_PER_MFMA, 0);
       }
-      if (pv_due) wa.template pv_lds<Tile>(slot((S + 3) & 3) + Tile::BYTES, va, pb);
-      if (live) {
-        wa.qk_ops(kop[0], 0, sc);
-        wa.qk_ops(kop[1], 1, sc);
-        wa.template read_vt<Tile>(slot(S) + Tile::BYTES, 0, va);
-        wa.softmax_tile(sl, sc, t >= nfull, ts, kend, pb);
+#endif
+#pragma unroll
+      for (int s2 = 0; s2 < NM; ++s2) {
+        wa.l[s2] += ls[s2];
+        scc[s2][0] = scn[s2][0];
+        scc[s2][1] = scn[s2][1];
       }
-    } else {
+      wa.template pv_lds<Tile>(vt, va, pb);
+      if (issuer && t + 2 < ntiles) {
+        if (t + 3 < ntiles) wait_vmcnt<PER_TILE>();
+        else wait_vmcnt<0>();
+      }
+      half_barrier();
+    };
+    // The last tile: softmax and PV only (no tile after it, no barrier).
+    auto last = [&](auto S_, int t) {
+      constexpr int S = decltype(S_)::value;
+      const int ts = k0 + kPreKeys * t;
+      if (t >= nfull) wa.mask_tile(scc, ts, kend);
+      const char* vt = slot(S) + Tile::BYTES;
+      u32x4 va[WA::VB];
+      u32x4 pb[NM];
+      wa.template read_vt<Tile>(vt, 0, va);
+      wa.softmax_tile(sl, scc, false, ts, kend, pb);
+      wa.template pv_lds<Tile>(vt, va, pb);
+    };
+    const int nlast = ntiles - 1;
+    for (int t = 0; t < nlast; t += 4) {
+      phase(std::integral_constant<int, 0>{}, t);
+      if (t + 1 >= nlast) break;
+      phase(std::integral_constant<int, 1>{}, t + 1);
+      if (t + 2 >= nlast) break;
+      phase(std::integral_constant<int, 2>{}, t + 2);
+      if (t + 3 >= nlast) break;
+      phase(std::integral_constant<int, 3>{}, t + 3);
+    }
+    switch (ntiles > 0 ? nlast & 3 : -1) {
+      case -1: break;  // no key: O = 0
+      case 0: last(std::integral_constant<int, 0>{}, nlast); break;
+      case 1: last(std::integral_constant<int, 1>{}, nlast); break;
+      case 2: last(std::integral_constant<int, 2>{}, nlast); break;
+      default: last(std::integral_constant<int, 3>{}, nlast); break;
+    }
+  } else {
+    // head_dim 256 (K operands in halves, V^T read in the phase of its PV):
+    // phase t issues tile t+2 into the slot of tile t-2, reads K(t) half by
+    // half around PV(t-1), runs QK(t) and forms P(t); before the barrier an
+    // issuing wave waits for its part of tile t+1 (vmcnt <= PER_TILE while
+    // tile t+2 is in flight).
+    u32x4 pb[NM];      // P of the previous tile, for its PV
+    u32x4 va[WA::VB];  // its V^T operands
+    bool pv_due = false;
+    auto step = [&](auto S_, int t) {
+      constexpr int S = decltype(S_)::value;
+      if (issuer && t + LEAD < ntiles) issue((S + LEAD) & 3, t + LEAD);
+      const int ts = k0 + kPreKeys * t;
+      const bool live = t < ntiles && ts < kend;
+      f32x4 sc[NM][2];
       u32x4 kh[WA::NC];
       if (live) wa.template k_operands<Tile>(slot(S), 0, kh);
       if (pv_due) {
@@ -1529,24 +1639,22 @@ __device__ __attribute__((always_inline)) inline void prefill_wg(const AttnArgs&
         wa.qk_ops(kh, 1, sc);
         wa.softmax_tile(sl, sc, t >= nfull, ts, kend, pb);
       }
+      pv_due = live;
+      if (issuer && t + 1 < ntiles) {
+        if (t + 2 < ntiles) wait_vmcnt<PER_TILE>();
+        else wait_vmcnt<0>();
+      }
+      half_barrier();
+    };
+    for (int t = 0; t <= ntiles; t += 4) {
+      step(std::integral_constant<int, 0>{}, t);
+      if (t + 1 > ntiles) break;
+      step(std::integral_constant<int, 1>{}, t + 1);
+      if (t + 2 > ntiles) break;
+      step(std::integral_constant<int, 2>{}, t + 2);
+      if (t + 3 > ntiles) break;
+      step(std::integral_constant<int, 3>{}, t + 3);
     }
-    pv_due = live;
-    if (issuer && t + 1 < ntiles) {
-      // tiles t+1 .. min(t+LEAD, ntiles-1) are in flight: all but t+1 may stay
-      if (LEAD > 2 && t + 3 < ntiles) wait_vmcnt<2 * PER_TILE>();
-      else if (t + 2 < ntiles) wait_vmcnt<PER_TILE>();
-      else wait_vmcnt<0>();
-    }
-    half_barrier();
-  };
-  for (int t = 0; t <= ntiles; t += 4) {
-    step(std::integral_constant<int, 0>{}, t);
-    if (t + 1 > ntiles) break;
-    step(std::integral_constant<int, 1>{}, t + 1);
-    if (t + 2 > ntiles) break;
-    step(std::integral_constant<int, 2>{}, t + 2);
-    if (t + 3 > ntiles) break;
-    step(std::integral_constant<int, 3>{}, t + 3);
   }
   float ltot[NM];
   wa.row_sums(ltot);
