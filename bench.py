@@ -911,8 +911,10 @@ def cpu_baseline(w, t, layer, budget_s, attn_bytes):
     q = t.q.cpu()
     nk = t.new_k.transpose(1, 2).squeeze(0).cpu()
     nv = t.new_v.transpose(1, 2).squeeze(0).cpu()
-    kc0 = t.kv_cache[layer, 0].cpu()
-    vc0 = t.kv_cache[layer, 1].cpu()
+    # the reference's eager path views the pool as contiguous [N, 16, Hkv, D]:
+    # a head-major pool is copied into that layout (same values)
+    kc0 = t.kv_cache[layer, 0].cpu().contiguous()
+    vc0 = t.kv_cache[layer, 1].cpu().contiguous()
     slots = t.slot_mapping.cpu()
     rows = eager.workload_rows(w)
     est = len(w.rows) * w.num_q_heads * sum(x.k_len for x in w.rows) * 4

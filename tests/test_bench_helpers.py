@@ -1,5 +1,6 @@
 """bench.py's host-side helpers, on the CPU: the launch description of an
-attention call is built from its launch list's unit counts."""
+attention call is built from its launch list's unit counts, and the CPU
+baseline runs on the head-major pool the headline uses."""
 import importlib.util
 import os
 
@@ -30,3 +31,19 @@ def test_launch_list_desc_names_every_launch(bench):
     assert "attn_prefill_kernel<BF16,128> x 8 units" in d  # 136 prefill units, 128 of them shared-prefix
     assert bench.launch_list_desc({"_schedules": {"k": None}}, _W()).endswith("(no launch list)")
     assert "decode" in bench.launch_list_desc({"_schedules": {"k": (None, 4096, 0, 0, 0, 0)}}, _W())
+
+
+def test_cpu_baseline_takes_a_head_major_pool(bench):
+    """The headline's pool is head-major (a strided view); the reference's
+    eager path views its pool as contiguous, so the baseline copies it into
+    that layout first."""
+    import dataclasses
+    import importlib
+
+    wl = importlib.import_module("serving-engine_amd.workloads")
+    w = wl.make_workload(2)
+    w = dataclasses.replace(w, rows=w.rows[:4])
+    t = wl.make_tensors(w, "cpu", num_layers=1, head_major=True)
+    assert not t.kv_cache.is_contiguous()
+    r = bench.cpu_baseline(w, t, 0, budget_s=0.5, attn_bytes=1e6)
+    assert r["value"] > 0 and r["kind"] == "port"
