@@ -1468,15 +1468,12 @@ __device__ __attribute__((always_inline)) inline void prefill_wg(const AttnArgs&
   };
 
   // One phase per tile, each ending in one work-group barrier (see the
-  // loop below).  The issuing waves put tile t+LEAD in flight at the start
+  // loops below).  The issuing waves put tile t+LEAD in flight at the start
   // of phase t; tile t sits in slot t % 4, and the loop body is unrolled
-  // four times so that every LDS access names a fixed slot.  (The two waves
-  // of a SIMD run the same phase and the hardware interleaves one's MFMAs
-  // with the other's softmax: a probe of this tile's MFMA, LDS and softmax
-  // work ran at 20 cycles per MFMA with one barrier per tile and 27 with
-  // the waves pinned half a tile apart by two barriers per tile; in this
-  // kernel the half-tile ping-pong measured 187.5 us against 182.6 on the
-  // mixed workload's prefill rows.)
+  // four times so that every LDS access names a fixed slot.  (Two barriers
+  // per tile, pinning the two waves of a SIMD half a tile apart, measured
+  // 187.5 us against 182.6 for one, on the mixed workload's prefill rows
+  // with 8-wave work-groups.)
   constexpr int PER_TILE = 2 * NI;  // DMA instructions per issuing wave and tile
   constexpr int LEAD = WA::NC <= 4 ? 3 : 2;
   const int ntiles = (kend_g - k0 + kPreKeys - 1) / kPreKeys;
@@ -1578,6 +1575,11 @@ __device__ __attribute__((always_inline)) inline void prefill_wg(const AttnArgs&
       }
       wa.template pv_lds<Tile>(vt, va, pb);
       if (issuer && t + 2 < ntiles) {
+        // This wave's vector memory operations in flight, oldest first: its
+        // PER_TILE DMAs of tile t+2 (issued in phase t-1), then, when it
+        // exists, its PER_TILE of tile t+3 (issued in this phase); nothing
+        // else (Q was waited for in the prologue).  Tile t+2 has landed once
+        // at most the newer PER_TILE remain.
         if (t + 3 < ntiles) wait_vmcnt<PER_TILE>();
         else wait_vmcnt<0>();
       }
@@ -1641,6 +1643,9 @@ __device__ __attribute__((always_inline)) inline void prefill_wg(const AttnArgs&
       }
       pv_due = live;
       if (issuer && t + 1 < ntiles) {
+        // In flight, oldest first: this wave's PER_TILE DMAs of tile t+1
+        // (issued in phase t-1), then its PER_TILE of tile t+2 (this phase)
+        // when it exists; tile t+1 has landed once at most PER_TILE remain.
         if (t + 2 < ntiles) wait_vmcnt<PER_TILE>();
         else wait_vmcnt<0>();
       }
