@@ -233,8 +233,8 @@ int kvhot_paged_attention(
     void* workspace, int64_t workspace_bytes,
     void* stream);
 
-/* Bytes of split-K partials kvhot_paged_attention_noalloc can hold (32 MiB). */
-#define KVHOT_NOALLOC_SCRATCH_BYTES (32LL << 20)
+/* Bytes of split-K partials kvhot_paged_attention_noalloc can hold (64 MiB). */
+#define KVHOT_NOALLOC_SCRATCH_BYTES (64LL << 20)
 
 /*
  * kvhot_paged_attention for callers that cannot allocate device memory (code

@@ -28,7 +28,7 @@ KVHOT_CAUSAL = 1
 KVHOT_DETERMINISTIC = 2
 
 # Split-K partials kvhot_paged_attention_noalloc holds (KVHOT_NOALLOC_SCRATCH_BYTES).
-NOALLOC_SCRATCH_BYTES = 32 << 20
+NOALLOC_SCRATCH_BYTES = 64 << 20
 
 _DTYPE_CODES = {
     torch.float32: KVHOT_F32,

@@ -2027,10 +2027,12 @@ static bool plan_decode(const int32_t* q_lens, const int32_t* k_lens, const int3
   std::vector<int64_t> pfx_sl(rows, 0), pfx_splits(rows, 0);
   for (const PrefixGroup& pg : pgroups) {
     const int64_t qblocks = (pg.nrows + prefix_queries - 1) / prefix_queries;
-    // Key splits for about half a device-fill of prefix work-groups: on 256
-    // rows sharing 1024 keys (D=128, G=4), 128 units beat 256 (half the fp32
-    // partials to write and fold) and 64 (units twice as long).
-    const int64_t units = std::max<int64_t>(groups / 2, 1);
+    // Key splits for a device-fill of prefix work-groups (a CU holds two
+    // 4-wave prefill work-groups where it holds one decode work-group): on
+    // 256 rows sharing 1024 keys (D=128, G=4), 512 units (8 splits) took
+    // 74.7 us per call against 76.2 with 256 and 78.2 with 128 (one box):
+    // shorter units outweigh the more fp32 partials to write and fold.
+    const int64_t units = std::max<int64_t>(2 * groups, 1);
     const int64_t want = (units + qblocks * Hkv - 1) / (qblocks * Hkv);
     const int64_t ks = std::max<int64_t>(1, std::min<int64_t>(want, pg.keys / kMinSplitKeys));
     for (int64_t r = pg.r0; r < pg.r0 + pg.nrows; ++r) {

@@ -133,9 +133,9 @@ def test_attention_checks_the_schedule_workspace(lib):
 
 @no_gpu
 def test_noalloc_rejects_calls_beyond_its_scratch(lib):
-    """The no-alloc variant holds at most 32 MiB of split-K partials; a call
+    """The no-alloc variant holds at most 64 MiB of split-K partials; a call
     that needs more is KVHOT_EWORKSPACE before it touches a device."""
-    assert sea_module("_lib").NOALLOC_SCRATCH_BYTES == 32 << 20
+    assert sea_module("_lib").NOALLOC_SCRATCH_BYTES == 64 << 20
     q3, c4, l2 = _i64(4096, 128, 1), _i64(16384, 1024, 128, 1), _i64(32, 1)
     f = FAKE
     # no schedule: 64 rows of up to 65536 keys in 32-key partitions -> 64 x 8 x 2048 partials of 2064 bytes
@@ -143,13 +143,13 @@ def test_noalloc_rejects_calls_beyond_its_scratch(lib):
             64, 64, 1, 65536, 32, 8, 128, 16, 1 << 20, 0.1, 1, 2, 32, None, 0, 0, 0, 0, 0, None]
     assert lib.kvhot_paged_attention_noalloc(*args) == -3
     msg = lib.kvhot_last_error()
-    assert str(64 * 8 * 2048 * 4 * 129 * 4).encode() in msg and b"33554432" in msg
+    assert str(64 * 8 * 2048 * 4 * 129 * 4).encode() in msg and b"67108864" in msg
     # a schedule whose merge units need one byte more than the scratch
     sched = list(args)
-    sched[29:35] = [f, 16, 0, 1, 0, (32 << 20) + 1]
+    sched[29:35] = [f, 16, 0, 1, 0, (64 << 20) + 1]
     assert lib.kvhot_paged_attention_noalloc(*sched) == -3
     # shared-prefix units alone (no merge units) need their partials too
-    sched[29:35] = [f, 16, 2, 0, 2, (32 << 20) + 1]
+    sched[29:35] = [f, 16, 2, 0, 2, (64 << 20) + 1]
     assert lib.kvhot_paged_attention_noalloc(*sched) == -3
     # invalid sizes are reported as such
     bad = list(args)
