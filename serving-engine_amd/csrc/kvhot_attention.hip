@@ -25,12 +25,14 @@
 //    loads are non-temporal: every byte of a call is read by one wave once.
 //  * attn_prefill_kernel<T, D, NM>: rows with q_len >= 2, and the key splits
 //    of a prefix shared by many decode rows (one unit serves all those rows'
-//    queries; the decode segments fold its partials in).  A work-group of 8
-//    waves per (row, kv head, query blocks) copies 32-key K/V tiles from the
-//    paged cache into LDS through a four-slot ring and shares them; both
-//    products use the 16x16x32 MFMA (P^T keeps S^T's key order as the K
-//    dimension).  Causal mask from q_pos_offset; tiles past the work-group's
-//    last query are never loaded.
+//    queries; the decode segments fold its partials in).  A work-group of 4
+//    waves (two per CU; 8 waves at head_dim 256) per (row, kv head, query
+//    block) copies 32-key K/V tiles from the paged cache into LDS through a
+//    four-slot ring and shares them; both products use the 16x16x32 MFMA
+//    (P^T keeps S^T's key order as the K dimension), and at head_dim <= 128
+//    the QK of the next tile runs beside the softmax of this one.  Causal
+//    mask from q_pos_offset; tiles past the work-group's last query are never
+//    loaded.
 //  * attn_generic_kernel<T>: VALU kernel for fp32 (exact fp32 arithmetic) and
 //    for shapes the MFMA kernels do not cover.
 #include "kvhot_internal.h"
