@@ -584,3 +584,27 @@ def test_deterministic_calls_repeat_bitwise(cuda, sea, wl, config, scheduled):
         outs.append((bits(o), l.cpu().numpy().view(np.int32)))
     assert np.array_equal(outs[0][0], outs[1][0]) and np.array_equal(outs[0][1], outs[1][1])
     assert_attention(w, o, l, ref_o, ref_l)
+
+
+def test_deterministic_cut_rows_repeat_bitwise(cuda, sea, wl):
+    """deterministic=True on a plan that cuts rows across work-groups (a few
+    long rows: parts joined by the merge launch): two calls give the same
+    bits, and match the oracle."""
+    w = custom(wl, [(1, 16384, 16383), (1, 12000, 11999), (1, 300, 299)], 32, 8, 128, torch.bfloat16)
+    announce("deterministic attention, 3 decode rows of up to 16384 keys (cut plan)")
+    T = wl.make_tensors(w, cuda)
+    ref_o, ref_l = oracle_step(w, T)
+    meta = wl.metadata_tensors(w, cuda)
+    cache = sea._PagedKVCache(T.kv_cache)
+    cache.write(T.new_k, T.new_v, 0, T.slot_mapping)
+    kc, vc = cache.blocks(0)
+    outs = []
+    for _ in range(2):
+        o, l = sea.paged_flash_attention(T.q, kc, vc, meta, w.num_q_heads, w.num_kv_heads,
+                                         1.0 / math.sqrt(w.head_dim), deterministic=True)
+        torch.cuda.synchronize()
+        outs.append((bits(o), l.cpu().numpy().view(np.int32)))
+    (plan,) = [p for p in meta["_schedules"].values() if p is not None]
+    assert plan[3] > 0  # merge units: the long rows were cut
+    assert np.array_equal(outs[0][0], outs[1][0]) and np.array_equal(outs[0][1], outs[1][1])
+    assert_attention(w, o, l, ref_o, ref_l)
