@@ -75,24 +75,25 @@ def check_attention(o, lse, ref_o, ref_lse, dtype):
 
 # ---------------------------------------------------------------- cases --
 
-def custom(wl, spec, hq, hkv, d, dtype, seed=3):
-    """spec: (q_len, k_len, q_pos_offset) rows over a shuffled pool."""
+def custom(wl, spec, hq, hkv, d, dtype, seed=3, bs=16):
+    """spec: (q_len, k_len, q_pos_offset) rows over a shuffled pool of
+    bs-token blocks."""
     rng = np.random.default_rng(seed)
-    need = [max(1, math.ceil(k / 16)) for _, k, _ in spec]
+    need = [max(1, math.ceil(k / bs)) for _, k, _ in spec]
     n = sum(need) + 7
     perm = rng.permutation(n)
     rows, k0 = [], 0
     for (ql, kl, off), nb in zip(spec, need):
         rows.append(wl.Row(ql, kl, off, perm[k0:k0 + nb].astype(np.int64), ql != 1))
         k0 += nb
-    return wl.Workload(0, "custom", dtype, hq, hkv, d, n, 1.0, rows, seed=seed)
+    return wl.Workload(0, "custom", dtype, hq, hkv, d, n, 1.0, rows, seed=seed, block_size=bs)
 
 
-def shared_custom(wl, spec, share, hq, hkv, d, dtype, seed=5):
+def shared_custom(wl, spec, share, hq, hkv, d, dtype, seed=5, bs=16):
     """custom() whose rows share leading blocks: share = [(first row, rows,
     blocks)], each such run of rows reading the same first `blocks` physical
     blocks."""
-    w = custom(wl, spec, hq, hkv, d, dtype, seed=seed)
+    w = custom(wl, spec, hq, hkv, d, dtype, seed=seed, bs=bs)
     n = w.num_blocks
     extra = sum(nb for _, _, nb in share)
     perm = np.random.default_rng(seed + 1).permutation(extra) + n
@@ -101,7 +102,7 @@ def shared_custom(wl, spec, share, hq, hkv, d, dtype, seed=5):
         common = perm[k:k + nb].astype(np.int64)
         k += nb
         for x in w.rows[r0:r0 + nrows]:
-            assert x.q_pos_offset >= nb * 16  # the row's own token lands past the shared blocks
+            assert x.q_pos_offset >= nb * bs  # the row's own token lands past the shared blocks
             x.block_table = np.concatenate([common, x.block_table[nb:]])
     w.num_blocks = n + extra
     return w

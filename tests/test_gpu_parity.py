@@ -47,16 +47,17 @@ def oracle_step(w, T, rows=None):
     rows = list(range(len(w.rows))) if rows is None else list(rows)
     keep = np.zeros(len(q_lens), dtype=bool)
     keep[rows] = True
-    need = [bt[r, : math.ceil(k_lens[r] / 16)] for r in rows if k_lens[r] > 0]
+    bs = w.block_size
+    need = [bt[r, : math.ceil(k_lens[r] / bs)] for r in rows if k_lens[r] > 0]
     used = np.unique(np.concatenate(need)) if need else np.zeros(1, np.int64)
     idx = torch.as_tensor(used, dtype=torch.int64, device=T.kv_cache.device)
     kc = f32(T.kv_cache[0, 0].index_select(0, idx))
     vc = f32(T.kv_cache[0, 1].index_select(0, idx))
     slots = T.slot_mapping.cpu().numpy()
-    blk, off = slots // 16, slots % 16
+    blk, off = slots // bs, slots % bs
     pos = np.searchsorted(used, blk)
     hit = (pos < len(used)) & (used[np.minimum(pos, len(used) - 1)] == blk)
-    new_slots = np.where(hit, pos * 16 + off, -1)
+    new_slots = np.where(hit, pos * bs + off, -1)
     nk = f32(T.new_k.transpose(1, 2).squeeze(0))
     nv = f32(T.new_v.transpose(1, 2).squeeze(0))
     kc, vc = paged_ref.reshape_and_cache(kc, vc, nk, nv, new_slots)
@@ -608,3 +609,24 @@ def test_deterministic_cut_rows_repeat_bitwise(cuda, sea, wl):
     assert plan[3] > 0  # merge units: the long rows were cut
     assert np.array_equal(outs[0][0], outs[1][0]) and np.array_equal(outs[0][1], outs[1][1])
     assert_attention(w, o, l, ref_o, ref_l)
+
+
+@pytest.mark.parametrize("bs,head_major", [(32, False), (48, False), (64, False), (32, True), (48, True)])
+def test_block_sizes(cuda, sea, wl, bs, head_major):
+    """Pools of 32-, 48- and 64-token blocks (the MFMA kernels take any
+    multiple of 16; a 16-key slice or half-tile then starts inside a block),
+    token-major and head-major: prefill chunks, decode rows sharing a prefix,
+    a long decode row and a short one in one batch, against the oracle."""
+    nb = -(-320 // bs)  # shared blocks: at least 320 keys
+    spec = [(96, 500, 404), (1, 700, 699), (1, 900, 899), (1, 1200, 1199), (1, 650, 649), (1, 1000, 999),
+            (1, 800, 799), (1, 6000, 5999), (1, 40, 39), (33, 33, 0)]
+    w = shared_custom(wl, spec, [(1, 6, nb)], 32, 8, 128, torch.bfloat16, seed=40 + bs, bs=bs)
+    announce(f"block_size {bs}, head_major={head_major}: mixed batch with 6 rows sharing {nb} blocks")
+    T = wl.make_tensors(w, cuda, head_major=head_major)
+    assert T.kv_cache.shape[3] == bs  # [layers, K/V, blocks, block_size, kv heads, head_dim]
+    ref_o, ref_l = oracle_step(w, T)
+    meta = wl.metadata_tensors(w, cuda)
+    o, l = hip_step(sea, wl, w, T, meta=meta)
+    assert_attention(w, o, l, ref_o, ref_l)
+    (plan,) = [p for p in meta["_schedules"].values() if p is not None]
+    assert plan[5] > 0 and plan[2] > plan[5]  # prefix units and prefill rows ran
