@@ -148,10 +148,11 @@ def test_update_writes_then_gathers(cuda, sea, head_major):
 
 # ------------------------------------------------------------- block copy --
 
-def test_copy_blocks_bit_exact(cuda, sea, wl):
+@pytest.mark.parametrize("bs", [16, 48])
+def test_copy_blocks_bit_exact(cuda, sea, wl, bs):
     w = wl.make_workload(4)
-    announce(f"copy_blocks {len(w.copy_src)} pairs x 2 layers")
-    kv = torch.empty(2, 2, w.num_blocks, 16, 8, 128, dtype=torch.bfloat16, device=cuda)
+    announce(f"copy_blocks {len(w.copy_src)} pairs x 2 layers, block_size {bs}")
+    kv = torch.empty(2, 2, w.num_blocks, bs, 8, 128, dtype=torch.bfloat16, device=cuda)
     kv.view(torch.int16).random_(generator=torch.Generator(device=cuda).manual_seed(9))
     before = bits(kv)
     sea._PagedKVCache(kv).copy_blocks(w.copy_src, w.copy_dst)
@@ -625,8 +626,13 @@ def test_block_sizes(cuda, sea, wl, bs, head_major):
     T = wl.make_tensors(w, cuda, head_major=head_major)
     assert T.kv_cache.shape[3] == bs  # [layers, K/V, blocks, block_size, kv heads, head_dim]
     ref_o, ref_l = oracle_step(w, T)
+    kb, vb = bits(T.kv_cache[0, 0]), bits(T.kv_cache[0, 1])
     meta = wl.metadata_tensors(w, cuda)
     o, l = hip_step(sea, wl, w, T, meta=meta)
     assert_attention(w, o, l, ref_o, ref_l)
+    # the append landed bit-exactly in the bs-token blocks
+    ek, ev = paged_ref.reshape_and_cache(kb, vb, bits(T.new_k.transpose(1, 2).squeeze(0)),
+                                         bits(T.new_v.transpose(1, 2).squeeze(0)), T.slot_mapping.cpu().numpy())
+    assert np.array_equal(bits(T.kv_cache[0, 0]), ek) and np.array_equal(bits(T.kv_cache[0, 1]), ev)
     (plan,) = [p for p in meta["_schedules"].values() if p is not None]
     assert plan[5] > 0 and plan[2] > plan[5]  # prefix units and prefill rows ran
