@@ -636,3 +636,22 @@ def test_block_sizes(cuda, sea, wl, bs, head_major):
     assert np.array_equal(bits(T.kv_cache[0, 0]), ek) and np.array_equal(bits(T.kv_cache[0, 1]), ev)
     (plan,) = [p for p in meta["_schedules"].values() if p is not None]
     assert plan[5] > 0 and plan[2] > plan[5]  # prefix units and prefill rows ran
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_block_size_8_runs_the_valu_kernel(cuda, sea, wl, dtype):
+    """8-token blocks (not a multiple of 16) take the VALU kernel: a prefill
+    chunk and decode rows against the oracle, the append bit-exact."""
+    spec = [(40, 100, 60), (1, 300, 299), (1, 17, 16), (1, 1000, 999)]
+    w = custom(wl, spec, 16, 4, 64, dtype, seed=50, bs=8)
+    announce(f"block_size 8, {dtype}: VALU kernel")
+    T = wl.make_tensors(w, cuda)
+    ref_o, ref_l = oracle_step(w, T)
+    kb, vb = bits(T.kv_cache[0, 0]), bits(T.kv_cache[0, 1])
+    meta = wl.metadata_tensors(w, cuda)
+    o, l = hip_step(sea, wl, w, T, meta=meta)
+    assert_attention(w, o, l, ref_o, ref_l)
+    assert all(p is None for p in meta["_schedules"].values())  # no MFMA launch list
+    ek, ev = paged_ref.reshape_and_cache(kb, vb, bits(T.new_k.transpose(1, 2).squeeze(0)),
+                                         bits(T.new_v.transpose(1, 2).squeeze(0)), T.slot_mapping.cpu().numpy())
+    assert np.array_equal(bits(T.kv_cache[0, 0]), ek) and np.array_equal(bits(T.kv_cache[0, 1]), ev)
