@@ -1260,7 +1260,6 @@ constexpr int kPreKeys = 32;
 #ifndef KVHOT_PRE_VALU_PER_MFMA
 #define KVHOT_PRE_VALU_PER_MFMA 4
 #endif
-constexpr int kPreSlots = 4;
 
 // A K (or V) tile in LDS: 32 key rows of 2*D bytes.  The 16-byte chunks of a
 // row are XOR-swizzled (chunk lc of row r sits at lc ^ swz(r)), so the MFMA
@@ -2363,6 +2362,8 @@ static void launch_mfma(const AttnArgs& a, int waves, int64_t rows, int64_t max_
         launched = true;
       }
     }
+#else
+    (void)waves;
 #endif
     if (!launched) launch_decode<TT, D, 8>(a, rows, n_dec, stream);
   }
