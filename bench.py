@@ -9,9 +9,10 @@ workload (64 rows, ctx U[128, 2048], 32/8 heads, D=128, bf16, block 16, pool
 256 MB Infinity Cache when it is read again.  The pool is the drop-in's
 documented one, allocate_kv_cache()'s default: the reference's
 [L, 2, N, 16, Hkv, D] shape and indexing with each block stored as
-[Hkv, 16, D] (head-major); `reference_layout` is the same calls on the
-reference's token-major [16, Hkv, D] blocks (--layout reference makes that
-the headline).
+[Hkv, 2, 16, D] (kv-interleaved: each kv head's 16 K rows, then its 16 V
+rows); `reference_layout` and `head_major_layout` are the same calls on the
+reference's token-major [16, Hkv, D] blocks and on head-major [Hkv, 16, D]
+blocks with the K and V pools apart (--layout makes either the headline).
 
 value = algorithmic bytes moved per step (K/V read + Q in + O out + block
 table + LSE out, plus the append's K/V read+write and slots) / step time, in
@@ -85,9 +86,18 @@ MFMA_BF16_PEAK_TFLOPS = 2500.0
 TRAFFIC_FILES = {
     "reference": os.path.join(ROOT, "profiles", "attention_decode_gqa64_traffic.md"),
     "head-major": os.path.join(ROOT, "profiles", "attention_decode_gqa64_headmajor_traffic.md"),
+    "kv-interleaved": os.path.join(ROOT, "profiles", "attention_decode_gqa64_kvinterleaved_traffic.md"),
 }
-LAYOUT_NAMES = {"head-major": "head-major blocks [Hkv, 16, D] (allocate_kv_cache's default)",
+LAYOUT_NAMES = {"kv-interleaved": "kv-interleaved blocks [Hkv, 2, 16, D]: each kv head's K rows, then its V rows "
+                                  "(allocate_kv_cache's default)",
+                "head-major": "head-major blocks [Hkv, 16, D], the K and V pools apart",
                 "reference": "the reference's token-major blocks [16, Hkv, D]"}
+# allocate_kv_cache's name of each --layout, and the line's key for its figures
+# when it is not the headline
+POOL_LAYOUT = {"kv-interleaved": "kv-interleaved", "head-major": "head-major", "reference": "token-major"}
+OTHER_KEYS = {"reference": "reference_layout", "head-major": "head_major_layout",
+              "kv-interleaved": "kv_interleaved_layout"}
+DEFAULT_POOL = "kv-interleaved"
 
 
 def parse():
@@ -96,9 +106,9 @@ def parse():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", type=int, default=2, choices=[2, 3, 4, 5])
-    ap.add_argument("--layout", choices=["head-major", "reference"], default="head-major",
-                    help="pool blocks stored [Hkv, 16, D] (allocate_kv_cache's default) or the reference's "
-                         "[16, Hkv, D]")
+    ap.add_argument("--layout", choices=sorted(LAYOUT_NAMES), default=DEFAULT_POOL,
+                    help="how the pool stores a block: kv-interleaved [Hkv, 2, 16, D] (allocate_kv_cache's "
+                         "default), head-major [Hkv, 16, D] or the reference's token-major [16, Hkv, D]")
     ap.add_argument("--layers", type=int, default=32)
     ap.add_argument("--partition-tokens", type=int, default=0)
     ap.add_argument("--kernel-reps", type=int, default=20,
@@ -305,8 +315,7 @@ def main():
 
     w = wl.make_workload(args.workload)
     layers = args.layers if args.workload != 5 else 1  # the 40 GB pool is one layer's
-    head_major = args.layout == "head-major"
-    t = wl.make_tensors(w, dev, num_layers=layers, head_major=head_major)
+    t = wl.make_tensors(w, dev, num_layers=layers, layout=POOL_LAYOUT[args.layout])
     cache = sea._PagedKVCache(t.kv_cache)
     meta = sea.build_paged_batch_metadata(w.scheduler_output(), device=dev)
     slots = meta["slot_mapping"]
@@ -348,21 +357,25 @@ def main():
     append_us, append_eager_us = per_call_us(
         lambda: [cache.write(t.new_k, t.new_v, i, slots) for i in range(layers)], layers, reps, dev)
 
-    other = deterministic = None
+    others, deterministic = {}, None
     if not args.headline_only:
-        # The same calls on a copy of the pool in the other block layout (same
-        # shape, values and results), and with deterministic=True.
-        other_layout = "reference" if head_major else "head-major"
-        kv2 = sea.allocate_kv_cache(layers, w.num_blocks, w.num_kv_heads, w.head_dim, dtype=w.dtype,
-                                    device=dev, head_major=not head_major)
-        kv2.copy_(t.kv_cache)
-        blocks2 = [(kv2[i, 0], kv2[i, 1]) for i in range(layers)]
-        o_us, _ = per_call_us(lambda: [attention(i, blocks2) for i in range(layers)], layers, reps, dev)
-        del kv2, blocks2
-        o_gbs = attn_bytes / (o_us * 1e-6) / 1e9
-        other = {"pool_layout": LAYOUT_NAMES[other_layout], "avg_launch_us": round(o_us, 3),
-                 "achieved": round(o_gbs, 2), "unit": "GB/s", "frac": round(o_gbs / HBM_PEAK_GBS, 4),
-                 "traffic": recorded_traffic(args.workload, other_layout)}
+        # The same calls on a copy of the pool in each other block layout
+        # (same shape, values and results), and with deterministic=True.
+        for other_layout in sorted(LAYOUT_NAMES):
+            if other_layout == args.layout:
+                continue
+            kv2 = sea.allocate_kv_cache(layers, w.num_blocks, w.num_kv_heads, w.head_dim, dtype=w.dtype,
+                                        device=dev, layout=POOL_LAYOUT[other_layout])
+            kv2.copy_(t.kv_cache)
+            blocks2 = [(kv2[i, 0], kv2[i, 1]) for i in range(layers)]
+            o_us, _ = per_call_us(lambda: [attention(i, blocks2) for i in range(layers)], layers, reps, dev)
+            del kv2, blocks2
+            torch.cuda.empty_cache()
+            o_gbs = attn_bytes / (o_us * 1e-6) / 1e9
+            others[OTHER_KEYS[other_layout]] = {
+                "pool_layout": LAYOUT_NAMES[other_layout], "avg_launch_us": round(o_us, 3),
+                "achieved": round(o_gbs, 2), "unit": "GB/s", "frac": round(o_gbs / HBM_PEAK_GBS, 4),
+                "traffic": recorded_traffic(args.workload, other_layout)}
         d_us, _ = per_call_us(lambda: [attention(i, deterministic=True) for i in range(layers)], layers, reps, dev)
         d_gbs = attn_bytes / (d_us * 1e-6) / 1e9
         deterministic = {"flag": "KVHOT_DETERMINISTIC (paged_flash_attention(..., deterministic=True))",
@@ -434,7 +447,7 @@ def main():
             "eager_call_us": round(attn_eager_us, 3),
             "pool_layout": LAYOUT_NAMES[args.layout],
         },
-        "reference_layout" if head_major else "head_major_pool": other,
+        **others,
         "deterministic": deterministic,
         "append": {"avg_launch_us": round(append_us, 3), "eager_call_us": round(append_eager_us, 3),
                    "algorithmic_bytes": append_bytes,
@@ -463,7 +476,7 @@ def append_leg(sea, wl, dev, reps, layers=16):
     import torch
 
     w = wl.make_workload(3)
-    t = wl.make_tensors(w, dev, num_layers=layers, head_major=True)
+    t = wl.make_tensors(w, dev, num_layers=layers, layout=POOL_LAYOUT[DEFAULT_POOL])
     cache = sea._PagedKVCache(t.kv_cache)
     slots = t.slot_mapping
     us, eager = per_call_us(lambda: [cache.write(t.new_k, t.new_v, i, slots) for i in range(layers)],
@@ -480,14 +493,14 @@ def append_leg(sea, wl, dev, reps, layers=16):
 
 
 def attention_leg(sea, wl, dev, config, layers, reps, calls=None):
-    """One attention call of workload `config` on head-major pools: per-call
+    """One attention call of workload `config` on the default pool layout: per-call
     time over `calls` back-to-back calls cycling through `layers` layer pools,
     GB/s of its algorithmic bytes (logical: every row's keys; unique: each
     physical K/V byte once) against 8 TB/s."""
     import torch
 
     w = wl.make_workload(config)
-    t = wl.make_tensors(w, dev, num_layers=layers, head_major=True)
+    t = wl.make_tensors(w, dev, num_layers=layers, layout=POOL_LAYOUT[DEFAULT_POOL])
     cache = sea._PagedKVCache(t.kv_cache)
     meta = sea.build_paged_batch_metadata(w.scheduler_output(), device=dev)
     blocks = [cache.blocks(i) for i in range(layers)]
@@ -509,7 +522,7 @@ def attention_leg(sea, wl, dev, config, layers, reps, calls=None):
     out = {"workload": w.name, "kernel": desc, "avg_call_us": round(us, 3), "eager_call_us": round(eager, 3),
            "algorithmic_bytes": logical, "achieved": round(logical / (us * 1e-6) / 1e9, 2), "peak": HBM_PEAK_GBS,
            "unit": "GB/s", "frac": round(logical / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
-           "pool_layout": LAYOUT_NAMES["head-major"],
+           "pool_layout": LAYOUT_NAMES[DEFAULT_POOL],
            "timing": f"HIP events over replays of one recorded graph of {calls} back-to-back calls over "
                      f"{layers} layer pool(s), median of {reps}"}
     if unique != logical:
@@ -611,7 +624,7 @@ def engine_measure(dev, steps=16, warmup=2, cpu_layers=(1, 2, 4)):
     cfg = _llama_8b_config(layers)
     model = _random_llama(cfg, dev, sea.register_attention())
     ctx, tables, n = _decode_batch(2 * (warmup + steps))
-    kv = sea.allocate_kv_cache(layers, n, 8, 128, dtype=torch.bfloat16, device=dev)  # head-major blocks
+    kv = sea.allocate_kv_cache(layers, n, 8, 128, dtype=torch.bfloat16, device=dev)  # the default layout
     gen = torch.Generator(device=dev)
     gen.manual_seed(1002)
     for lyr in range(layers):  # synthetic context K/V, N(0, 1) / sqrt(128)
@@ -785,7 +798,7 @@ def prefill_measure(sea, wl, dev, reps, layers=16):
     decode = dataclasses.replace(full, rows=[r for r in full.rows if not r.prefill])
     out = {}
     for key, w in (("prefill_rows", rows), ("decode_rows", decode), ("mixed_batch", full)):
-        t = wl.make_tensors(w, dev, num_layers=layers, head_major=True)
+        t = wl.make_tensors(w, dev, num_layers=layers, layout=POOL_LAYOUT[DEFAULT_POOL])
         cache = sea._PagedKVCache(t.kv_cache)
         meta = sea.build_paged_batch_metadata(w.scheduler_output(), device=dev)
         blocks = [cache.blocks(i) for i in range(layers)]
@@ -912,7 +925,7 @@ def cpu_baseline(w, t, layer, budget_s, attn_bytes):
     nk = t.new_k.transpose(1, 2).squeeze(0).cpu()
     nv = t.new_v.transpose(1, 2).squeeze(0).cpu()
     # the reference's eager path views the pool as contiguous [N, 16, Hkv, D]:
-    # a head-major pool is copied into that layout (same values)
+    # a pool in another block layout is copied into that one (same values)
     kc0 = t.kv_cache[layer, 0].cpu().contiguous()
     vc0 = t.kv_cache[layer, 1].cpu().contiguous()
     slots = t.slot_mapping.cpu()

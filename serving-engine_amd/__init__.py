@@ -17,6 +17,7 @@ from .paged_attention_kernel import (
 )
 from .model_runner import (
     PAGED_HIP_ATTN_IMPL,
+    POOL_LAYOUTS,
     _PagedKVCache,
     allocate_kv_cache,
     forward_step,
@@ -45,6 +46,7 @@ __all__ = [
     "Scheduler",
     "SchedulerOutput",
     "_PagedKVCache",
+    "POOL_LAYOUTS",
     "allocate_kv_cache",
     "build_paged_batch_metadata",
     "build_slot_mapping",

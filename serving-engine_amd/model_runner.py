@@ -152,11 +152,20 @@ class _PagedKVCache:
         kv = self.kv_cache
         es = kv.element_size()
         block_bytes = kv[0, 0, 0].numel() * es
-        if not _dense(kv[0, 0, 0]):
-            raise ValueError("each block's [block_size, Hkv, D] payload must fill one dense range")
+        if _dense(kv[0, 0, 0]):
+            # K and V of a block each fill one range: the launch copies both
+            kv_bytes = kv.stride(1) * es
+        elif _dense(kv[0, :, 0]) and kv[0, :, 0].storage_offset() == kv.storage_offset():
+            # a kv-interleaved pool: K and V of a block fill one range together,
+            # starting at K's first element; its two halves are copied as "K"
+            # and "V"
+            kv_bytes = block_bytes
+        else:
+            raise ValueError("each block's [block_size, Hkv, D] payload, or its K and V together, "
+                             "must fill one dense range")
         lib = _lib.load()
         status = lib.kvhot_copy_blocks(
-            kv.data_ptr(), kv.shape[0], kv.stride(0) * es, kv.stride(1) * es,
+            kv.data_ptr(), kv.shape[0], kv.stride(0) * es, kv_bytes,
             kv.stride(2) * es, block_bytes, n, src.data_ptr(), dst.data_ptr(),
             src.numel(), _lib.stream_handle(dev))
         _lib.check(status, "kvhot_copy_blocks")
@@ -190,7 +199,7 @@ def register_attention(name: str = PAGED_HIP_ATTN_IMPL) -> str:
 
 def _dense(t):
     """Whether t's elements fill one dense range of memory in some order of
-    its dimensions (a block's payload in either pool layout)."""
+    its dimensions (a block's payload, or a block's K and V together)."""
     dims = sorted((st, sz) for st, sz in zip(t.stride(), t.shape) if sz > 1)
     span = 1
     for st, sz in dims:
@@ -200,23 +209,44 @@ def _dense(t):
     return True
 
 
+POOL_LAYOUTS = ("kv-interleaved", "head-major", "token-major")
+
+
 def allocate_kv_cache(num_layers, num_blocks, num_kv_heads, head_dim, dtype=torch.bfloat16,
-                      device="cuda", block_size=BLOCK_SIZE, head_major=True):
+                      device="cuda", block_size=BLOCK_SIZE, head_major=None, layout="kv-interleaved"):
     """Zero-filled pool [L, 2, N, block_size, Hkv, D] (serving_engine/model_runner.py:101-110).
 
-    head_major=True (the default) keeps that shape and indexing but stores
-    each block as [Hkv, block_size, D] (the tensor is a transposed view), so
-    the 16 rows of one kv head in a block are one contiguous 2*16*D-byte
-    range.  Decode reads a block one kv head at a time, and in the
-    reference's token-major order (head_major=False) a head's rows sit at a
-    fixed offset inside each token's [Hkv, D] row, which on MI355X maps some
-    heads to slower HBM channels than others: the 64-row GQA decode call
-    takes about 6% longer on that layout.  Every entry point takes either."""
-    if head_major:
-        return torch.zeros(num_layers, 2, num_blocks, num_kv_heads, block_size, head_dim,
-                           dtype=dtype, device=device).transpose(3, 4)
-    return torch.zeros(num_layers, 2, num_blocks, block_size, num_kv_heads, head_dim,
-                       dtype=dtype, device=device)
+    Every layout keeps that shape and indexing (the tensor is a view with the
+    layout's strides, and every kvhot entry point takes strides); they differ
+    in how a block lies in memory:
+
+    * "kv-interleaved" (the default): block n stores, for each kv head, its
+      block_size K rows and then its block_size V rows ([L, N, Hkv, 2,
+      block_size, D] in memory), so the K and V of one kv head in one block
+      -- what a decode wave reads per slice -- are one contiguous range of
+      2 * 2 * block_size * D bytes;
+    * "head-major": the K and V pools apart, each block [Hkv, block_size, D];
+    * "token-major": the reference's blocks, [block_size, Hkv, D].
+
+    In the reference's order a head's rows sit at a fixed offset inside each
+    token's [Hkv, D] row, which on MI355X maps some heads to slower HBM
+    channels than others.  Measured on the 64-row GQA decode call: 53.1 us
+    token-major, 49.0 head-major, 48.5 kv-interleaved (the 16-row 32k-token
+    call: 375 us head-major, 343-356 kv-interleaved).
+
+    head_major (the older keyword): True for "head-major", False for
+    "token-major"."""
+    if head_major is not None:
+        layout = "head-major" if head_major else "token-major"
+    shape = dict(dtype=dtype, device=device)
+    if layout == "kv-interleaved":
+        return torch.zeros(num_layers, num_blocks, num_kv_heads, 2, block_size, head_dim, **shape).permute(
+            0, 3, 1, 4, 2, 5)
+    if layout == "head-major":
+        return torch.zeros(num_layers, 2, num_blocks, num_kv_heads, block_size, head_dim, **shape).transpose(3, 4)
+    if layout == "token-major":
+        return torch.zeros(num_layers, 2, num_blocks, block_size, num_kv_heads, head_dim, **shape)
+    raise ValueError(f"unknown pool layout {layout!r}; one of {POOL_LAYOUTS}")
 
 
 def num_blocks_for_memory(free_bytes, num_layers, num_kv_heads, head_dim, dtype=torch.bfloat16,

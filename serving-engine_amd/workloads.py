@@ -250,18 +250,23 @@ class Tensors:
     slot_mapping: torch.Tensor  # int64 [T]
 
 
-def make_tensors(w: Workload, device="cuda", num_layers: int = 1, head_major: bool = False) -> Tensors:
+def make_tensors(w: Workload, device="cuda", num_layers: int = 1, head_major: bool = False,
+                 layout: str | None = None) -> Tensors:
     """Pool with every used block filled with seeded N(0,1)*value_scale values
-    (other blocks zero), plus Q and the K/V to append.  head_major: the pool
-    stores each block as [Hkv, block_size, D] (same shape and values)."""
+    (other blocks zero), plus Q and the K/V to append.  layout: how the pool
+    stores a block (allocate_kv_cache's layouts; the same shape and values
+    in each); without it, "head-major" if head_major else the reference's
+    "token-major"."""
+    from .model_runner import allocate_kv_cache
+
     device = torch.device(device)
     gen = torch.Generator(device=device)
     gen.manual_seed(w.seed)
     hkv, d, bs = w.num_kv_heads, w.head_dim, w.block_size
-    if head_major:
-        kv = torch.zeros(num_layers, 2, w.num_blocks, hkv, bs, d, dtype=w.dtype, device=device).transpose(3, 4)
-    else:
-        kv = torch.zeros(num_layers, 2, w.num_blocks, bs, hkv, d, dtype=w.dtype, device=device)
+    if layout is None:
+        layout = "head-major" if head_major else "token-major"
+    kv = allocate_kv_cache(num_layers, w.num_blocks, hkv, d, dtype=w.dtype, device=device, block_size=bs,
+                           layout=layout)
     used = torch.as_tensor(w.used_blocks(), dtype=torch.int64, device=device)
     for layer in range(num_layers):
         for kvi in range(2):

@@ -1,6 +1,6 @@
 """bench.py's host-side helpers, on the CPU: the launch description of an
 attention call is built from its launch list's unit counts, and the CPU
-baseline runs on the head-major pool the headline uses."""
+baseline runs on the strided pools the headline uses."""
 import importlib.util
 import os
 
@@ -33,8 +33,9 @@ def test_launch_list_desc_names_every_launch(bench):
     assert "decode" in bench.launch_list_desc({"_schedules": {"k": (None, 4096, 0, 0, 0, 0)}}, _W())
 
 
-def test_cpu_baseline_takes_a_head_major_pool(bench):
-    """The headline's pool is head-major (a strided view); the reference's
+@pytest.mark.parametrize("layout", ["kv-interleaved", "head-major"])
+def test_cpu_baseline_takes_a_strided_pool(bench, layout):
+    """The headline's pool is kv-interleaved (a strided view); the reference's
     eager path views its pool as contiguous, so the baseline copies it into
     that layout first."""
     import dataclasses
@@ -43,7 +44,15 @@ def test_cpu_baseline_takes_a_head_major_pool(bench):
     wl = importlib.import_module("serving-engine_amd.workloads")
     w = wl.make_workload(2)
     w = dataclasses.replace(w, rows=w.rows[:4])
-    t = wl.make_tensors(w, "cpu", num_layers=1, head_major=True)
+    t = wl.make_tensors(w, "cpu", num_layers=1, layout=layout)
     assert not t.kv_cache.is_contiguous()
     r = bench.cpu_baseline(w, t, 0, budget_s=0.5, attn_bytes=1e6)
     assert r["value"] > 0 and r["kind"] == "port"
+
+
+def test_bench_layouts_match_the_allocator(bench):
+    import importlib
+
+    sea = importlib.import_module("serving-engine_amd")
+    assert bench.DEFAULT_POOL == "kv-interleaved" and set(bench.POOL_LAYOUT.values()) == set(sea.POOL_LAYOUTS)
+    assert set(bench.LAYOUT_NAMES) == set(bench.POOL_LAYOUT) == set(bench.OTHER_KEYS)

@@ -121,15 +121,15 @@ def test_append_int32_slots_padding_and_strides(cuda, sea, dtype):
     assert np.array_equal(bits(kv[1, 1]), ev)
 
 
-@pytest.mark.parametrize("head_major", [False, True])
-def test_update_writes_then_gathers(cuda, sea, head_major):
+@pytest.mark.parametrize("layout", ["token-major", "head-major", "kv-interleaved"])
+def test_update_writes_then_gathers(cuda, sea, layout):
     """_PagedKVCache.update, the eager path's write then dense gather
-    (reference serving_engine/model_runner.py:34-40), on both pool layouts:
+    (reference serving_engine/model_runner.py:34-40), on every pool layout:
     the layer's K/V bit-exactly as the oracle's append leaves them, and the
     gathered rows bit-exactly those slots of the flat [N * 16, Hkv, D] view."""
-    announce(f"_PagedKVCache.update, head_major={head_major}")
+    announce(f"_PagedKVCache.update, {layout} pool")
     g = torch.Generator(device=cuda).manual_seed(17)
-    kv = sea.allocate_kv_cache(2, 12, 4, 64, dtype=torch.bfloat16, device=cuda, head_major=head_major)
+    kv = sea.allocate_kv_cache(2, 12, 4, 64, dtype=torch.bfloat16, device=cuda, layout=layout)
     kv.view(torch.int16).random_(generator=g)
     key = torch.randn(1, 4, 7, 64, generator=g, device=cuda).to(torch.bfloat16)
     val = torch.randn(1, 4, 7, 64, generator=g, device=cuda).to(torch.bfloat16)
@@ -299,24 +299,27 @@ def test_config3_mixed_prefill_decode(cuda, sea, wl):
     assert_attention(w, o, l, ref_o, ref_l)
 
 
-@pytest.mark.parametrize("config", [2, 3])
-def test_head_major_pool(cuda, sea, wl, config):
-    """The pool stored block-wise as [Hkv, 16, D] (allocate_kv_cache(head_major=True)):
-    same shape and values, other strides; append, attention and block copy
-    give what they give on the reference's layout."""
+@pytest.mark.parametrize("config,layout", [(2, "head-major"), (3, "head-major"), (2, "kv-interleaved"),
+                                           (3, "kv-interleaved"), (4, "kv-interleaved")])
+def test_strided_pool_layouts(cuda, sea, wl, config, layout):
+    """The pool stored block-wise as [Hkv, 16, D] (head-major) or [Hkv, 2, 16,
+    D] (kv-interleaved, allocate_kv_cache's default): same shape and values,
+    other strides; append, attention and block copy give what they give on
+    the reference's layout."""
     w = wl.make_workload(config)
-    announce(f"attention workload {config} on a head-major pool")
-    T = wl.make_tensors(w, cuda, head_major=True)
-    assert T.kv_cache.stride()[3:] == (w.head_dim, 16 * w.head_dim, 1)
+    announce(f"attention workload {config} on a {layout} pool")
+    T = wl.make_tensors(w, cuda, layout=layout)
+    heads = 16 * w.head_dim * (2 if layout == "kv-interleaved" else 1)
+    assert T.kv_cache.stride()[3:] == (w.head_dim, heads, 1)
     ref_o, ref_l = oracle_step(w, T)
     meta = sea.build_paged_batch_metadata(w.scheduler_output(), device=cuda) if config == 3 else None
     o, l = hip_step(sea, wl, w, T, meta=meta)
     assert_attention(w, o, l, ref_o, ref_l)
-    # the append landed in the head-major slots bit-exactly
+    # the append landed in the slots bit-exactly
     slots = T.slot_mapping.cpu()
     kc = T.kv_cache[0, 0].reshape(-1, w.num_kv_heads, w.head_dim)
     assert torch.equal(kc[slots.to(cuda)].cpu(), T.new_k.transpose(1, 2).squeeze(0).cpu())
-    # block copy moves whole head-major blocks
+    # block copy moves whole blocks, K and V
     cache = sea._PagedKVCache(T.kv_cache)
     before = T.kv_cache.clone()
     src = int(slots[0]) // 16
@@ -612,18 +615,20 @@ def test_deterministic_cut_rows_repeat_bitwise(cuda, sea, wl):
     assert_attention(w, o, l, ref_o, ref_l)
 
 
-@pytest.mark.parametrize("bs,head_major", [(32, False), (48, False), (64, False), (32, True), (48, True)])
-def test_block_sizes(cuda, sea, wl, bs, head_major):
+@pytest.mark.parametrize("bs,layout", [(32, "token-major"), (48, "token-major"), (64, "token-major"),
+                                       (32, "head-major"), (48, "head-major"), (48, "kv-interleaved"),
+                                       (64, "kv-interleaved")])
+def test_block_sizes(cuda, sea, wl, bs, layout):
     """Pools of 32-, 48- and 64-token blocks (the MFMA kernels take any
     multiple of 16; a 16-key slice or half-tile then starts inside a block),
-    token-major and head-major: prefill chunks, decode rows sharing a prefix,
+    in each pool layout: prefill chunks, decode rows sharing a prefix,
     a long decode row and a short one in one batch, against the oracle."""
     nb = -(-320 // bs)  # shared blocks: at least 320 keys
     spec = [(96, 500, 404), (1, 700, 699), (1, 900, 899), (1, 1200, 1199), (1, 650, 649), (1, 1000, 999),
             (1, 800, 799), (1, 6000, 5999), (1, 40, 39), (33, 33, 0)]
     w = shared_custom(wl, spec, [(1, 6, nb)], 32, 8, 128, torch.bfloat16, seed=40 + bs, bs=bs)
-    announce(f"block_size {bs}, head_major={head_major}: mixed batch with 6 rows sharing {nb} blocks")
-    T = wl.make_tensors(w, cuda, head_major=head_major)
+    announce(f"block_size {bs}, {layout} pool: mixed batch with 6 rows sharing {nb} blocks")
+    T = wl.make_tensors(w, cuda, layout=layout)
     assert T.kv_cache.shape[3] == bs  # [layers, K/V, blocks, block_size, kv heads, head_dim]
     ref_o, ref_l = oracle_step(w, T)
     kb, vb = bits(T.kv_cache[0, 0]), bits(T.kv_cache[0, 1])
