@@ -23,6 +23,11 @@
  *                          (serving_engine/paged_attention_kernel.py:189-197)
  *   GQA: query head h reads kv head h / (num_q_heads / num_kv_heads)
  *        (serving_engine/paged_attention_kernel.py:81).
+ * Those are the logical shapes: every entry point takes the pool's strides,
+ * so a block may lie in memory token-major (the reference's [block_size,
+ * num_kv_heads, head_dim]), head-major ([num_kv_heads, block_size,
+ * head_dim]) or kv-interleaved (K and V of one block together,
+ * [num_kv_heads, 2, block_size, head_dim]: the fastest for decode).
  */
 #ifndef KVHOT_H
 #define KVHOT_H
@@ -93,7 +98,9 @@ int kvhot_reshape_and_cache(const void* key, const int64_t key_strides[3],
  * dst_block_ids[i]:  kv_cache[:, :, dst[i]] = kv_cache[:, :, src[i]].
  * The whole-pool tensor is described by its base pointer and BYTE strides of
  * its first three dims (layer, K/V, block); each block's payload of
- * block_bytes bytes must be contiguous.  Destinations must be unique and must
+ * block_bytes bytes must be contiguous.  (A kv-interleaved pool, whose K and
+ * V of one block are one range of 2 * block_bytes, is copied by passing half
+ * of that range as block_bytes and its offset as the K/V stride.)  Destinations must be unique and must
  * not appear among the sources of the same call (the copies run in parallel).
  * Ids outside [0, num_blocks) are skipped.
  * The reference has no block copy: fork() shares blocks by reference count
