@@ -35,7 +35,8 @@ its own layer pools:
   private tails U[64, 512]), GB/s on the unique K/V bytes (the shared prefix
   once) and on the logical ones (every row's keys);
 * long_context: the long-context workload (16 rows x 32,768 tokens over a
-  40 GB pool, 512-token split-K partitions), GB/s;
+  40 GB pool, 512-token split-K partitions), GB/s; `planner_split` the same
+  call with the planner choosing the split (the drop-in's default);
 * prefill: the chunked-prefill rows of the mixed workload (8 x 512-token
   chunks on contexts U[0, 4096]): one attention call over them, FLOPs
   counted over visible (query, key) pairs only, against the 2.5 PFLOP/s
@@ -496,7 +497,10 @@ def attention_leg(sea, wl, dev, config, layers, reps, calls=None):
     """One attention call of workload `config` on the default pool layout: per-call
     time over `calls` back-to-back calls cycling through `layers` layer pools,
     GB/s of its algorithmic bytes (logical: every row's keys; unique: each
-    physical K/V byte once) against 8 TB/s."""
+    physical K/V byte once) against 8 TB/s.  A workload with fixed split-K
+    partitions (the long-context one's 512 tokens) is also timed with the
+    planner choosing the split (`planner_split`: paged_flash_attention
+    without partition_tokens)."""
     import torch
 
     w = wl.make_workload(config)
@@ -517,6 +521,19 @@ def attention_leg(sea, wl, dev, config, layers, reps, calls=None):
     logical = w.decode_algorithmic_bytes()
     unique = w.decode_algorithmic_bytes(unique=True)
     desc = launch_list_desc(meta, w)
+    planner = None
+    if pt:
+        meta2 = sea.build_paged_batch_metadata(w.scheduler_output(), device=dev)
+
+        def body2():
+            for c in range(calls):
+                kc, vc = blocks[c % layers]
+                sea.paged_flash_attention(t.q, kc, vc, meta2, w.num_q_heads, w.num_kv_heads, scale)
+
+        us2, _ = per_call_us(body2, calls, reps, dev)
+        planner = {"kernel": launch_list_desc(meta2, w), "avg_call_us": round(us2, 3),
+                   "achieved": round(logical / (us2 * 1e-6) / 1e9, 2), "unit": "GB/s",
+                   "frac": round(logical / (us2 * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
     del t, cache, blocks
     torch.cuda.empty_cache()
     out = {"workload": w.name, "kernel": desc, "avg_call_us": round(us, 3), "eager_call_us": round(eager, 3),
@@ -531,6 +548,7 @@ def attention_leg(sea, wl, dev, config, layers, reps, calls=None):
         out["unique_frac"] = round(unique / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)
     if pt:
         out["partition_tokens"] = pt
+        out["planner_split"] = planner
     return out
 
 
