@@ -81,7 +81,8 @@ struct AttnArgs {
   // (row, partition, head group) and work-groups without work exit.
   const int4* sched;
   const int4* merge_units;  // schedule: two int4 per split decode segment
-  int32_t dec_slots;  // LDS (LSE, O) slots of a decode work-group, >= its waves
+  int32_t dec_slots;  // LDS (LSE, O) slots of a decode work-group, >= its ranges
+  int32_t dec_ranges; // range descriptors per decode work-group (its waves, or 4x them)
   // KVHOT_DETERMINISTIC: every decode wave walks exactly its planned range,
   // in order (no claiming from other waves), so each partial sum, and with it
   // out and lse, is the same bits on every call.
@@ -626,18 +627,18 @@ __host__ __device__ inline int decode_splits(int nslices, int W, int Hkv) {
   return S;
 }
 
-// LDS of a decode work-group with S slots, in 4-byte words: per slot the
-// normalised O [G][D] and base-2 LSE [G] of its query heads and its segment
-// key (row, kv head, part); per wave the claim counter, range end and segment
-// description [8]; the slot-pool counter.
+// LDS of a decode work-group with P ranges and S slots, in 4-byte words: per
+// slot the normalised O [G][D] and base-2 LSE [G] of its query heads and its
+// segment key (row, kv head, part); per range the claim counter, range end
+// and segment description [8]; the slot-pool counter.
 constexpr int kDecInfo = 8;
 // Bit of a decode descriptor's part field: the segment folds in its row's
 // shared-prefix partials.
 constexpr int kPrefixFold = 0x8000;
 // Prefix partials a fold reads per round trip.
 constexpr int kFoldBatch = 8;
-__host__ __device__ constexpr int64_t decode_lds_words(int64_t W, int64_t S, int64_t G, int64_t D) {
-  return S * G * D + S * G + 4 * S + (2 + kDecInfo) * W + 1;
+__host__ __device__ constexpr int64_t decode_lds_words(int64_t P, int64_t S, int64_t G, int64_t D) {
+  return S * G * D + S * G + 4 * S + (2 + kDecInfo) * P + 1;
 }
 
 __device__ inline int wave_max_int(int x) {
@@ -661,6 +662,7 @@ __device__ __attribute__((always_inline)) inline void decode_wg(const AttnArgs& 
   const int G = a.G;
   const int PT = a.part_tokens;
   const int S = a.dec_slots;
+  const int P = a.dec_ranges;  // ranges: wave w starts on range w (w < W <= P)
   const bool fixed = a.fixed != 0;
 
   // ---- this wave's range: slices [s0, s1) of part `part` of (row, kvh) ----
@@ -673,7 +675,7 @@ __device__ __attribute__((always_inline)) inline void decode_wg(const AttnArgs& 
     // 15 set (kPrefixFold): the row's shared prefix left `parts` partials
     // from index pidx in an earlier launch; this segment, the rest of the
     // row, folds them in and writes the row's output.
-    const int4* u = sched + 2 * (static_cast<int64_t>(bx) * W + wave);
+    const int4* u = sched + 2 * (static_cast<int64_t>(bx) * P + wave);
     const int4 u0 = u[0], u1 = u[1];
     const int x = __builtin_amdgcn_readfirstlane(u0.x);
     const int y = __builtin_amdgcn_readfirstlane(u0.y);
@@ -737,10 +739,10 @@ __device__ __attribute__((always_inline)) inline void decode_wg(const AttnArgs& 
   float* so = smem;                                      // [S][G][D]
   float* sl = so + static_cast<int64_t>(S) * G * D;      // [S][G]
   int* skey = reinterpret_cast<int*>(sl + S * G);        // [S][4] row, kvh, part, -
-  int* cnt = skey + 4 * S;                               // [W] next slice to claim
-  int* dend = cnt + W;                                   // [W] end of the range
-  int* info = dend + W;                                  // [W][kDecInfo]
-  int* nslot = info + kDecInfo * W;                      // slots handed out
+  int* cnt = skey + 4 * S;                               // [P] next slice to claim
+  int* dend = cnt + P;                                   // [P] end of the range
+  int* info = dend + P;                                  // [P][kDecInfo]
+  int* nslot = info + kDecInfo * P;                      // slots handed out
 
   const int bs = a.bs;
   auto block_of = [&](int r, int slice) -> int64_t {     // physical block of a slice
@@ -769,9 +771,37 @@ __device__ __attribute__((always_inline)) inline void decode_wg(const AttnArgs& 
     dend[wave] = s0 + nsl;
     int* d = info + kDecInfo * wave;
     d[0] = krow; d[1] = kvh; d[2] = part; d[3] = nparts;
-    d[4] = static_cast<int>(qs); d[5] = kend; d[6] = 0; d[7] = 0;
+    d[4] = static_cast<int>(qs); d[5] = kend; d[6] = static_cast<int>(pidx); d[7] = 1;
     skey[4 * wave] = -1;
-    if (wave == 0) *nslot = W;
+    if (wave == 0) *nslot = P;
+  }
+  // Ranges past the first W (launch lists of fixed partitions): wave w sets up
+  // ranges w + W, w + 2W, ...; they start untouched (d[7] = 0), each with its
+  // own slot, the one of the same index.
+  for (int r = wave + W; r < P; r += W) {
+    const int4* u = sched + 2 * (static_cast<int64_t>(bx) * P + r);
+    const int4 u0 = u[0], u1 = u[1];
+    const int x = __builtin_amdgcn_readfirstlane(u0.x);
+    const int y = __builtin_amdgcn_readfirstlane(u0.y);
+    const int rr = x >= 0 ? (x & 0xffff) : -1, rnp = (x >> 16) & 0xffff;
+    const int rh = y & 0xffff, rp = (y >> 16) & 0xffff;
+    const int rs0 = __builtin_amdgcn_readfirstlane(u0.z), rs1 = __builtin_amdgcn_readfirstlane(u0.w);
+    const int rqs = __builtin_amdgcn_readfirstlane(u1.x), rke = __builtin_amdgcn_readfirstlane(u1.y);
+    const int rpi = __builtin_amdgcn_readfirstlane(u1.w);
+    const bool rfold = (rp & kPrefixFold) != 0;
+    const bool rvalid = x >= 0 && rh < a.Hkv && rqs >= 0 && rqs < a.total_q && rs0 >= 0 && rnp >= 1 &&
+                        (rfold ? rp == kPrefixFold && rpi >= 0 && static_cast<int64_t>(rpi) + rnp <= a.num_partials
+                               : rp < rnp && (rnp == 1 || (rpi >= 0 && rpi < a.num_partials)));
+    const int rke2 = min(rke, 16 * rs1);
+    const int rn = rvalid && rke2 > 16 * rs0 ? (rke2 - 16 * rs0 + 15) / 16 : 0;
+    if (lane == 0) {
+      cnt[r] = rs0;
+      dend[r] = rs0 + rn;
+      int* d = info + kDecInfo * r;
+      d[0] = rvalid ? rr : -1; d[1] = rh; d[2] = rp; d[3] = rnp;
+      d[4] = rqs; d[5] = rke; d[6] = rpi; d[7] = 0;
+      skey[4 * r] = -1;
+    }
   }
   // LDS-only barrier: the first slice's loads stay in flight across it.
   __asm__ volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
@@ -787,7 +817,7 @@ __device__ __attribute__((always_inline)) inline void decode_wg(const AttnArgs& 
   // same_segment), or -1.
   auto pick = [&](bool same_segment) -> int {
     int best = -1;
-    if (lane < W) {
+    if (lane < P) {
       const int left = dend[lane] - cnt[lane];
       const int* d = info + kDecInfo * lane;
       bool ok = left > 0;
@@ -824,6 +854,7 @@ __device__ __attribute__((always_inline)) inline void decode_wg(const AttnArgs& 
 
 #if KVHOT_DECODE_DEPTH < 2
   int cv = wave;           // range being claimed from
+  int own = wave;          // the last of this wave's own ranges it entered (deterministic order)
   bool live = nsl > 0;     // the current segment may still have slices
   for (;;) {
     int j = -1;
@@ -856,12 +887,32 @@ __device__ __attribute__((always_inline)) inline void decode_wg(const AttnArgs& 
       continue;
     }
     have = false;
-    // Segment exhausted: park its state, then take slices of another one.
+    // Segment exhausted: park its state, then take slices of another one:
+    // the range with the most left, or with KVHOT_DETERMINISTIC the wave's
+    // own next range (ranges w + W, w + 2W, ... of a launch list of fixed
+    // partitions), in order.
     if (used) flush();
-    if (fixed) break;
-    const int v = pick(false);
+    int v = -1;
+    if (fixed) {
+      for (own += W; own < P; own += W)
+        if (__builtin_amdgcn_readfirstlane(dend[own] - cnt[own]) > 0) {
+          v = own;
+          break;
+        }
+    } else {
+      v = pick(false);
+    }
     if (v < 0) break;
-    if (used) {
+    // The first wave to enter a range parks its state in the range's own
+    // slot; a later one takes a slot from the pool (none left: it stops,
+    // and the range's other waves finish it).
+    int first = 0;
+    if (lane == 0) first = atomicExch(&info[kDecInfo * v + 7], 1) == 0 ? 1 : 0;
+    first = __builtin_amdgcn_readlane(first, 0);
+    if (first) {
+      slot = v;
+      used = false;
+    } else if (used) {
       int ns = 0;
       if (lane == 0) ns = atomicAdd(nslot, 1);
       ns = __builtin_amdgcn_readlane(ns, 0);
@@ -980,76 +1031,96 @@ __device__ __attribute__((always_inline)) inline void decode_wg(const AttnArgs& 
 #endif
   __syncthreads();
 
-  // ---- merge: the first wave of each segment combines the segment's slots ----
-  if (!valid) return;
-  if (wave > 0) {
-    const int* d = info + kDecInfo * (wave - 1);
-    if (d[0] == row && d[1] == kvh && d[2] == part) return;
-  }
+  // ---- merge: each range's slots are combined by the wave that set the
+  // range up (a segment split over several ranges: by the first of them) ----
   const int nused = min(__builtin_amdgcn_readfirstlane(*nslot), S);
-  const bool mine = lane < nused && skey[4 * lane] == row && skey[4 * lane + 1] == kvh &&
-                    skey[4 * lane + 2] == part;
-  const uint64_t slots = __ballot(mine);
-  for (int it = lane; it < G * (D / 4); it += 64) {
-    const int hh = it / (D / 4);
-    const int d0 = 4 * (it % (D / 4));
-    // The slots' states, weighted against their maximum.
-    float mx = -INFINITY;
-    for (uint64_t b = slots; b; b &= b - 1) mx = fmaxf(mx, sl[__builtin_ctzll(b) * G + hh]);
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-    float lsum = 0.f;
-    if (mx != -INFINITY) {
-      for (uint64_t b = slots; b; b &= b - 1) {
-        const int w = __builtin_ctzll(b);
-        const float wt = fast_exp2(sl[w * G + hh] - mx);
-        lsum += wt;
-        acc += wt * *reinterpret_cast<const f32x4*>(so + (static_cast<int64_t>(w) * G + hh) * D + d0);
-      }
-    }
-    if (fold) {
-      // The prefix partials, kFoldBatch at a time with all their loads in
-      // flight together (indices past the last partial re-read it, weight 0),
-      // combined with a running maximum.
-      for (int p0 = 0; p0 < nparts; p0 += kFoldBatch) {
-        float lp[kFoldBatch];
-        f32x4 ov[kFoldBatch];
-#pragma unroll
-        for (int k = 0; k < kFoldBatch; ++k) {
-          const int64_t pi = pidx + min(p0 + k, nparts - 1);
-          lp[k] = a.ws_lse[pi * G + hh];
-          ov[k] = *reinterpret_cast<const f32x4*>(a.ws_o + (pi * G + hh) * D + d0);
-        }
-        float cm = mx;
-#pragma unroll
-        for (int k = 0; k < kFoldBatch; ++k) {
-          if (p0 + k >= nparts) lp[k] = -INFINITY;
-          cm = fmaxf(cm, lp[k]);
-        }
-        if (cm == -INFINITY) continue;
-        const float sc = mx == -INFINITY ? 0.f : fast_exp2(mx - cm);
-        acc *= sc;
-        lsum *= sc;
-#pragma unroll
-        for (int k = 0; k < kFoldBatch; ++k) {
-          const float wt = lp[k] == -INFINITY ? 0.f : fast_exp2(lp[k] - cm);
+  auto merge = [&](int mrow, int mkvh, int mpart, int mnp, int64_t mpidx, int64_t mqs) {
+    const bool mfold = (mpart & kPrefixFold) != 0;
+    const bool mine = lane < nused && skey[4 * lane] == mrow && skey[4 * lane + 1] == mkvh &&
+                      skey[4 * lane + 2] == mpart;
+    const uint64_t slots = __ballot(mine);
+    for (int it = lane; it < G * (D / 4); it += 64) {
+      const int hh = it / (D / 4);
+      const int d0 = 4 * (it % (D / 4));
+      // The slots' states, weighted against their maximum.
+      float mx = -INFINITY;
+      for (uint64_t b = slots; b; b &= b - 1) mx = fmaxf(mx, sl[__builtin_ctzll(b) * G + hh]);
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+      float lsum = 0.f;
+      if (mx != -INFINITY) {
+        for (uint64_t b = slots; b; b &= b - 1) {
+          const int w = __builtin_ctzll(b);
+          const float wt = fast_exp2(sl[w * G + hh] - mx);
           lsum += wt;
-          acc += wt * ov[k];
+          acc += wt * *reinterpret_cast<const f32x4*>(so + (static_cast<int64_t>(w) * G + hh) * D + d0);
         }
-        mx = cm;
+      }
+      if (mfold) {
+        // The prefix partials, kFoldBatch at a time with all their loads in
+        // flight together (indices past the last partial re-read it, weight 0),
+        // combined with a running maximum.
+        for (int p0 = 0; p0 < mnp; p0 += kFoldBatch) {
+          float lp[kFoldBatch];
+          f32x4 ov[kFoldBatch];
+#pragma unroll
+          for (int k = 0; k < kFoldBatch; ++k) {
+            const int64_t pi = mpidx + min(p0 + k, mnp - 1);
+            lp[k] = a.ws_lse[pi * G + hh];
+            ov[k] = *reinterpret_cast<const f32x4*>(a.ws_o + (pi * G + hh) * D + d0);
+          }
+          float cm = mx;
+#pragma unroll
+          for (int k = 0; k < kFoldBatch; ++k) {
+            if (p0 + k >= mnp) lp[k] = -INFINITY;
+            cm = fmaxf(cm, lp[k]);
+          }
+          if (cm == -INFINITY) continue;
+          const float sc = mx == -INFINITY ? 0.f : fast_exp2(mx - cm);
+          acc *= sc;
+          lsum *= sc;
+#pragma unroll
+          for (int k = 0; k < kFoldBatch; ++k) {
+            const float wt = lp[k] == -INFINITY ? 0.f : fast_exp2(lp[k] - cm);
+            lsum += wt;
+            acc += wt * ov[k];
+          }
+          mx = cm;
+        }
+      }
+      const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
+      const int h = mkvh * G + hh;
+      const float lse2 = lsum > 0.f ? mx + __log2f(lsum) : -INFINITY;
+      if (mnp == 1 || mfold) {
+        st* dp = static_cast<st*>(a.o) + mqs * a.o_st + static_cast<int64_t>(h) * a.o_sh + d0;
+        *reinterpret_cast<u32x2*>(dp) =
+            u32x2{TT::pack2(acc.x * inv, acc.y * inv), TT::pack2(acc.z * inv, acc.w * inv)};
+        if (a.lse && d0 == 0) a.lse[mqs * a.l_st + static_cast<int64_t>(h) * a.l_sh] = lse2 * kLn2;
+      } else {
+        *reinterpret_cast<f32x4*>(a.ws_o + (mpidx * G + hh) * D + d0) = acc * inv;
+        if (d0 == 0) a.ws_lse[mpidx * G + hh] = lse2;
       }
     }
-    const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
-    const int h = kvh * G + hh;
-    const float lse2 = lsum > 0.f ? mx + __log2f(lsum) : -INFINITY;
-    if (nparts == 1 || fold) {
-      st* dp = static_cast<st*>(a.o) + qs * a.o_st + static_cast<int64_t>(h) * a.o_sh + d0;
-      *reinterpret_cast<u32x2*>(dp) =
-          u32x2{TT::pack2(acc.x * inv, acc.y * inv), TT::pack2(acc.z * inv, acc.w * inv)};
-      if (a.lse && d0 == 0) a.lse[qs * a.l_st + static_cast<int64_t>(h) * a.l_sh] = lse2 * kLn2;
-    } else {
-      *reinterpret_cast<f32x4*>(a.ws_o + (pidx * G + hh) * D + d0) = acc * inv;
-      if (d0 == 0) a.ws_lse[pidx * G + hh] = lse2;
+  };
+  // (Each range's description is read back from LDS rather than held in
+  // registers through the loop; without a launch list the partial index is
+  // recomputed, as it may not fit the table's 32 bits.)
+  for (int r = wave; r < P; r += W) {
+    const int* d = info + kDecInfo * r;
+    const int mrow = __builtin_amdgcn_readfirstlane(d[0]);
+    if (mrow < 0) continue;
+    const int mkvh = __builtin_amdgcn_readfirstlane(d[1]);
+    const int mpart = __builtin_amdgcn_readfirstlane(d[2]);
+    const int mnp = __builtin_amdgcn_readfirstlane(d[3]);
+    const int64_t mqs = __builtin_amdgcn_readfirstlane(d[4]);
+    const int64_t mpidx = sched ? static_cast<int64_t>(__builtin_amdgcn_readfirstlane(d[6]))
+                                : (static_cast<int64_t>(mrow) * a.Hkv + mkvh) * a.max_parts + mpart;
+    bool dup = false;
+    for (int r2 = 0; r2 < r; ++r2) {
+      const int* d2 = info + kDecInfo * r2;
+      dup = dup || (d2[0] == mrow && d2[1] == mkvh && d2[2] == mpart);
     }
+    if (__builtin_amdgcn_readfirstlane(static_cast<int>(dup)) != 0) continue;
+    merge(mrow, mkvh, mpart, mnp, mpidx, mqs);
   }
 }
 
@@ -1796,25 +1867,43 @@ static int decode_waves(int64_t G, int64_t D) {
   return 8;
 }
 
-// LDS bytes a decode work-group of W waves may use (see kMaxLdsBytes).
-static int64_t decode_lds_limit(int W, int64_t G, int64_t D) {
-  return decode_lds_words(W, W, G, D) * 4 <= kMaxLdsBytes ? kMaxLdsBytes : kCuLdsBytes;
+// LDS bytes a decode work-group of P ranges may use (see kMaxLdsBytes).
+static int64_t decode_lds_limit(int P, int64_t G, int64_t D) {
+  return decode_lds_words(P, P, G, D) * 4 <= kMaxLdsBytes ? kMaxLdsBytes : kCuLdsBytes;
 }
 
-// LDS slots of a decode work-group of W waves: one per wave plus a pool of up
-// to 3W more for waves that move on to other segments, as LDS allows; 0 when
-// one slot per wave does not fit.  (A wave that finds the pool empty stops
-// taking slices of other segments.  With many short segments per work-group
-// -- 256 rows' private tails after a shared prefix -- a pool of 3W rather
-// than W took the call from 75.1 to 74.4 us, one box; at most 4W slots keeps
-// the merge's 64-lane ballot over them.)
-static int decode_slots(int W, int64_t G, int64_t D) {
-  const int64_t limit = decode_lds_limit(W, G, D);
-  const int64_t base = decode_lds_words(W, W, G, D);
+// LDS slots of a decode work-group of W waves and P ranges: one per range
+// plus a pool of up to 3W more for waves that move on to ranges another wave
+// entered first, as LDS allows; 0 when one slot per range does not fit.  (A
+// wave that finds the pool empty stops taking slices of other segments.
+// With many short segments per work-group -- 256 rows' private tails after
+// a shared prefix -- a pool of 3W rather than W took the call from 75.1 to
+// 74.4 us, one box; P + 3W <= 64 keeps the merge's 64-lane ballot over the
+// slots.)
+static int decode_slots(int W, int P, int64_t G, int64_t D) {
+  const int64_t limit = decode_lds_limit(P, G, D);
+  const int64_t base = decode_lds_words(P, P, G, D);
   if (base * 4 > limit) return 0;
   const int64_t spare = limit / 4 - base;
   const int64_t per_slot = G * D + G + 4;
-  return W + static_cast<int>(std::max<int64_t>(0, std::min<int64_t>(3 * W, spare / per_slot)));
+  return P + static_cast<int>(std::max<int64_t>(0, std::min<int64_t>(3 * W, spare / per_slot)));
+}
+
+// Range descriptors per decode work-group of W waves.  A launch list of
+// fixed partitions (partition_tokens > 0) gives a work-group up to
+// kFixedRangesPerWave ranges per wave, one partition each: a wave starts on
+// one and, when it is used up, enters the range with the most slices left,
+// parking each partition's state in that range's own slot; so a device-full
+// of work-groups takes a long-context call in one round, where one
+// partition per wave took four (16 rows x 32,768 tokens, 512-token
+// partitions: 1,024 work-groups of 8 one-partition waves).  Other launch
+// lists, the grid path and two-slice waves keep one range per wave.
+constexpr int kFixedRangesPerWave = 4;
+static int decode_ranges(int W, int64_t G, int64_t D, bool fixed_partitions) {
+  const int P = kFixedRangesPerWave * W;
+  if (!fixed_partitions || KVHOT_DECODE_DEPTH >= 2 || P + 3 * W > 64) return W;
+  if (decode_slots(W, P, G, D) < P) return W;
+  return P;
 }
 
 // Bytes of one split-K partial: the normalised O and LSE of G query heads.
@@ -1870,7 +1959,7 @@ constexpr int prefill_nm(int64_t D) { return D == 64 ? 4 : (D == 128 ? KVHOT_PRE
 template <class TT, int D, int W>
 static int decode_groups_per_cu(int64_t G) {
   int n = 0;
-  const size_t lds = static_cast<size_t>(decode_lds_words(W, decode_slots(W, G, D), G, D) * 4);
+  const size_t lds = static_cast<size_t>(decode_lds_words(W, decode_slots(W, W, G, D), G, D) * 4);
   if ((lds > kMaxLdsBytes &&
        hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_decode_kernel<TT, D, W>),
                            hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)) != hipSuccess) ||
@@ -2011,7 +2100,7 @@ static std::vector<PrefixGroup> find_prefix_groups(const int32_t* q_starts, cons
 
 static bool plan_decode(const int32_t* q_lens, const int32_t* k_lens, const int32_t* q_offs,
                         const int32_t* q_starts, const int32_t* bt, int64_t bt_stride, int64_t bs,
-                        int64_t rows, int64_t Hkv, bool causal, int W, int64_t groups,
+                        int64_t rows, int64_t Hkv, bool causal, int W, int ranges, int64_t groups,
                         int64_t given_pt, int64_t slice_bytes, int64_t prefix_queries, std::vector<int4>& dec,
                         std::vector<int4>& mrg, std::vector<int4>& pfx, int64_t& partials) {
   dec.clear();
@@ -2066,9 +2155,12 @@ static bool plan_decode(const int32_t* q_lens, const int32_t* k_lens, const int3
   // Adds slices [s, s + rem) of segment seg (row r, kv head h) to the open
   // work-groups: whole when it is a fixed partition p, else cut at the
   // work-group loads.
+  // Pieces per work-group: one per wave, or with fixed partitions one per
+  // range (decode_ranges).
+  const int cap = given_pt > 0 ? ranges : W;
   auto place = [&](int seg, int64_t r, int64_t h, int64_t s, int64_t rem, int64_t p, bool splittable) {
     for (;;) {
-      if (static_cast<int>(cur.size()) == W) close();
+      if (static_cast<int>(cur.size()) == cap) close();
       const int64_t space = target - load;
       if (rem <= space + slack || (!splittable && cur.empty())) {
         const int part = splittable ? seg_parts[seg]++ : static_cast<int>(p);
@@ -2251,8 +2343,12 @@ static bool plan_decode(const int32_t* q_lens, const int32_t* k_lens, const int3
     }
   }
 
+  // Descriptors per work-group: W (one range per wave), or `ranges` when the
+  // plan has fixed partitions (padded with empty ranges).
+  const int per_wg = given_pt > 0 ? ranges : W;
   for (const auto& g : wgs) {
-    // Waves per piece: one each, the rest to the piece with most slices per wave.
+    // Waves per piece: one each, the rest to the piece with most slices per
+    // wave (more pieces than waves: one range each).
     const int k = static_cast<int>(g.size());
     std::vector<int> w(k, 1);
     for (int extra = W - k; extra > 0; --extra) {
@@ -2281,6 +2377,11 @@ static bool plan_decode(const int32_t* q_lens, const int32_t* k_lens, const int3
         dec.push_back(int4{r | (nparts << 16), pc.kvh | (part << 16), a0, a1});
         dec.push_back(int4{q_starts[r], static_cast<int>(kend[r]), first, pidx});
       }
+    }
+    const int emitted = std::max(k, W);
+    for (int e = emitted; e < per_wg; ++e) {
+      dec.push_back(int4{-1, 0, 0, 0});
+      dec.push_back(int4{0, 0, -1, 0});
     }
   }
   return true;
@@ -2315,12 +2416,13 @@ static void plan_prefill(const int32_t* q_lens, const int32_t* k_lens, const int
 
 template <class TT, int D, int W>
 static void launch_decode(const AttnArgs& a, int64_t rows, int64_t n_dec, hipStream_t stream) {
-  dim3 grid = a.sched ? dim3(static_cast<uint32_t>(n_dec / W))
+  AttnArgs da = a;
+  da.dec_ranges = a.sched && a.dec_ranges > W && n_dec % a.dec_ranges == 0 ? a.dec_ranges : W;
+  dim3 grid = a.sched ? dim3(static_cast<uint32_t>(n_dec / da.dec_ranges))
                       : dim3(static_cast<uint32_t>(a.Hkv), static_cast<uint32_t>(a.max_parts),
                              static_cast<uint32_t>(rows));
-  AttnArgs da = a;
-  da.dec_slots = decode_slots(W, a.G, D);
-  const size_t lds = static_cast<size_t>(decode_lds_words(W, da.dec_slots, a.G, D) * 4);
+  da.dec_slots = decode_slots(W, da.dec_ranges, a.G, D);
+  const size_t lds = static_cast<size_t>(decode_lds_words(da.dec_ranges, da.dec_slots, a.G, D) * 4);
   if (lds > kMaxLdsBytes)
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_decode_kernel<TT, D, W>),
                               hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
@@ -2434,8 +2536,9 @@ extern "C" int64_t kvhot_paged_attention_schedule(
     const int64_t G = num_q_heads / num_kv_heads;
     const int64_t groups = resident_decode_waves(dtype, head_dim, pl.waves, G) / pl.waves;
     const int64_t prefix_queries = prefill_waves(head_dim) * 16 * prefill_nm(head_dim) / G;  // per prefill work-group
+    const int ranges = decode_ranges(pl.waves, G, head_dim, partition_tokens > 0);
     if (plan_decode(q_lens, k_lens, q_pos_offsets, q_starts, block_table, bt_row_stride, block_size,
-                    num_rows, num_kv_heads, is_causal, pl.waves, groups, partition_tokens,
+                    num_rows, num_kv_heads, is_causal, pl.waves, ranges, groups, partition_tokens,
                     32 * head_dim * dtype_size(dtype), prefix_queries, dec, mrg, pfx, partials)) {
       plan_prefill(q_lens, k_lens, q_pos_offsets, num_rows, num_kv_heads, G, head_dim, is_causal, pre);
       pre.insert(pre.begin(), pfx.begin(), pfx.end());  // shared-prefix units first
@@ -2587,6 +2690,11 @@ static int paged_attention_impl(
       a.part_tokens = pl.part_tokens;
       a.max_parts = pl.max_parts;
     }
+    // A launch list of fixed partitions groups its decode ranges as the
+    // planner did (the same partition_tokens is passed to both calls; with
+    // another value the ranges come in groups of one per wave, which gives
+    // the same results).
+    a.dec_ranges = schedule ? decode_ranges(pl.waves, a.G, head_dim, partition_tokens > 0) : pl.waves;
 #define KVHOT_MFMA(TT, DD) \
   launch_mfma<TT, DD>(a, pl.waves, num_rows, max_q_len, n_dec, n_pre, n_mrg, n_pfx, s)
     if (dtype == KVHOT_BF16) {

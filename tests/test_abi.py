@@ -508,6 +508,34 @@ def test_schedule_shared_prefix_units(lib):
     assert len(set(allp)) == len(allp) and max(allp) < nparts_total
 
 
+def test_schedule_fixed_partitions_give_work_groups_several_ranges_per_wave(lib):
+    """A launch list of fixed partitions (16 rows x 32768 keys, 512-token
+    partitions, as the long-context workload) gives each decode work-group up
+    to four ranges per wave, one partition each, so that a device-full of
+    work-groups takes the call in one round: 256 work-groups of 32 ranges,
+    1024 slices each.  Without fixed partitions the same rows keep one range
+    per wave."""
+    rows, keys, pt = 16, 32768, 512
+    k_lens = [keys] * rows
+    dec, pre, merge, ws, qs = _schedule(lib, [1] * rows, k_lens, [k - 1 for k in k_lens], pt=pt)
+    P = 4 * W
+    assert len(dec) == GROUPS * P and all(w is not None for w in dec)
+    _check_decode_schedule(dec, merge, ws, qs, W, {r: keys for r in range(rows)}, 8, pt=pt)
+    for g in range(0, len(dec), P):
+        ranges = dec[g:g + P]
+        assert sum(w["s1"] - w["s0"] for w in ranges) == keys * rows * 8 // 16 // GROUPS
+        # one partition per range
+        assert all(w["s1"] - w["s0"] == pt // 16 and w["s0"] == w["part"] * pt // 16 for w in ranges)
+    assert sorted(merge[:, 2].tolist()) == [keys // pt] * (rows * 8)
+    # a few short rows: their work-groups are padded to 32 ranges with empty ones
+    dec, pre, merge, ws, qs = _schedule(lib, [1, 1, 1], [300, 40, 2000], [299, 39, 1999], pt=64)
+    assert len(dec) % P == 0
+    _check_decode_schedule(dec, merge, ws, qs, W, {0: 300, 1: 40, 2: 2000}, 8, pt=64)
+    # the planner's own split: one range per wave
+    dec, pre, merge, ws, qs = _schedule(lib, [1] * rows, k_lens, [k - 1 for k in k_lens])
+    assert len(dec) == GROUPS * W
+
+
 def test_schedule_long_rows_sharing_a_short_prefix_fill_the_device(lib):
     """A few long rows whose tables share a short prefix: their tails are cut
     across work-groups like unshared rows (the prefix partials join each cut

@@ -615,6 +615,28 @@ def test_deterministic_cut_rows_repeat_bitwise(cuda, sea, wl):
     assert_attention(w, o, l, ref_o, ref_l)
 
 
+def test_deterministic_fixed_partitions_repeat_bitwise(cuda, sea, wl):
+    """deterministic=True with fixed 128-token partitions (work-groups of
+    several ranges per wave, each wave walking its own in order): two calls
+    give the same bits, and match the oracle."""
+    w = wl.make_workload(2)
+    announce("deterministic attention, workload 2, 128-token partitions")
+    T = wl.make_tensors(w, cuda)
+    ref_o, ref_l = oracle_step(w, T)
+    meta = wl.metadata_tensors(w, cuda)
+    cache = sea._PagedKVCache(T.kv_cache)
+    cache.write(T.new_k, T.new_v, 0, T.slot_mapping)
+    kc, vc = cache.blocks(0)
+    outs = []
+    for _ in range(2):
+        o, l = sea.paged_flash_attention(T.q, kc, vc, meta, w.num_q_heads, w.num_kv_heads,
+                                         1.0 / math.sqrt(w.head_dim), partition_tokens=128, deterministic=True)
+        torch.cuda.synchronize()
+        outs.append((bits(o), l.cpu().numpy().view(np.int32)))
+    assert np.array_equal(outs[0][0], outs[1][0]) and np.array_equal(outs[0][1], outs[1][1])
+    assert_attention(w, o, l, ref_o, ref_l)
+
+
 @pytest.mark.parametrize("bs,layout", [(32, "token-major"), (48, "token-major"), (64, "token-major"),
                                        (32, "head-major"), (48, "head-major"), (48, "kv-interleaved"),
                                        (64, "kv-interleaved")])
