@@ -154,7 +154,8 @@ def launch_list_desc(meta, w):
     if n_pre > n_pfx:
         parts.append(f"attn_prefill_kernel<{tt},{w.head_dim}> x {n_pre - n_pfx} units")
     if n_dec:
-        parts.append(f"attn_decode_kernel<{tt},{w.head_dim}> x {n_dec} waves")
+        # one range per wave, or up to four per wave with fixed partitions
+        parts.append(f"attn_decode_kernel<{tt},{w.head_dim}> x {n_dec} ranges")
     if n_mrg:
         parts.append(f"attn_merge_kernel<{tt},{w.head_dim}> x {n_mrg} units")
     return "one attention call: " + " + ".join(parts)
