@@ -157,9 +157,11 @@ int64_t kvhot_paged_attention_workspace_bytes(
  * laid end to end and cut into equal numbers of 16-token slices per decode
  * work-group, one device-full of work-groups; a range cut in two becomes
  * "parts" in different work-groups.  Units of 8 int32, in order:
- * num_decode_units per-wave descriptors (whole work-groups; each carries its
- * row's metadata and first block, so the wave's first K/V loads depend on
- * nothing else), num_prefill_units per-work-group prefill units (longest
+ * num_decode_units range descriptors (whole work-groups: one per wave, or
+ * with partition_tokens > 0 up to four per wave; each carries its row's
+ * metadata and first block, so the wave's first K/V loads depend on nothing
+ * else -- the kernel checks that block against the device block table before
+ * using it), num_prefill_units per-work-group prefill units (longest
  * first), num_merge_units units, one per decode range cut into parts.
  * Shared prefixes: when at least 4 decode rows (with causal masking or not)
  * read the same first 256 or more keys through the same physical blocks, the

@@ -762,6 +762,13 @@ __device__ __attribute__((always_inline)) inline void decode_wg(const AttnArgs& 
   int i = s0;              // slice whose loads are in flight, if `have`
   bool have = nsl > 0;     // the first slice of the range is taken without a claim
 #if KVHOT_DECODE_DEPTH < 2
+  // The first slice's block comes from the launch list, built from the host
+  // copy of the block table, so that its loads wait for nothing.  The device
+  // table's entry is read before them and compared before the slice is used:
+  // a caller that edited only the device table gets the slice loaded again
+  // from the block the device table names.
+  bool check_first = sched && have && d_first >= 0;
+  const int64_t dev_first = check_first ? block_of(row, s0) : 0;
   if (have)
     wa.load_slice(a, kvh, d_first >= 0 ? min(static_cast<int64_t>(d_first), a.num_blocks - 1) : block_of(row, s0),
                   kb % bs, T);
@@ -870,6 +877,11 @@ __device__ __attribute__((always_inline)) inline void decode_wg(const AttnArgs& 
     }
     // The next slice's block id is fetched while this slice's loads land.
     const int64_t jb = j >= 0 ? block_of(__builtin_amdgcn_readfirstlane(krow), __builtin_amdgcn_readfirstlane(j)) : 0;
+    if (check_first) {
+      check_first = false;
+      const int64_t want = __builtin_amdgcn_readfirstlane(static_cast<int>(dev_first));
+      if (want != min(static_cast<int64_t>(d_first), a.num_blocks - 1)) wa.load_slice(a, kvh, want, kb % bs, T);
+    }
     if (have) {
       wa.compute_slice(a, 16 * i, kkend, INT_MAX, T);
       used = true;
@@ -1020,8 +1032,10 @@ __device__ __attribute__((always_inline)) inline void decode_wg(const AttnArgs& 
   // half-step leaves them (a block-table entry, then a buffer's K/V).
   claim_next();
   {
-    const bool h0 = __builtin_amdgcn_readfirstlane(static_cast<int>(have && d_first >= 0)) != 0;
-    wa.load_slice(a, kvh, h0 ? min(static_cast<int64_t>(d_first), a.num_blocks - 1) : 0, kb % bs, T, h0);
+    // (The first block from the device table, which the launch list's copy
+    // may not match.)
+    const bool h0 = __builtin_amdgcn_readfirstlane(static_cast<int>(have)) != 0;
+    wa.load_slice(a, kvh, h0 ? block_of(row, s0) : 0, kb % bs, T, h0);
   }
   for (;;) {
     half(T1, iy, hy);

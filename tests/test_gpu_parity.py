@@ -8,6 +8,7 @@ of 1e-2 (16-bit) or 1e-5 (fp32) (tests/parity.py; tests/test_parity_bound.py
 shows that this check rejects one wrong block per row).  Full-size workloads
 1-5 run as generated; every case prints its name before touching the GPU.
 """
+import dataclasses
 import math
 
 import numpy as np
@@ -613,6 +614,28 @@ def test_deterministic_cut_rows_repeat_bitwise(cuda, sea, wl):
     assert plan[3] > 0  # merge units: the long rows were cut
     assert np.array_equal(outs[0][0], outs[1][0]) and np.array_equal(outs[0][1], outs[1][1])
     assert_attention(w, o, l, ref_o, ref_l)
+
+
+def test_device_block_table_edit_not_in_the_host_copy(cuda, sea, wl):
+    """The launch list carries each decode range's first physical block from
+    the host copy of the block table; a caller that then edits only the
+    device table (here: rows 0 and 1 swap their first blocks) still gets the
+    attention the device table describes, because the kernel checks that
+    block against the device table before using it."""
+    w = wl.make_workload(2)
+    announce("attention workload 2, first blocks of rows 0 and 1 swapped on the device only")
+    T = wl.make_tensors(w, cuda)
+    meta = wl.metadata_tensors(w, cuda)
+    bt = meta["block_table"]
+    a, b = int(bt[0, 0]), int(bt[1, 0])
+    assert a != b
+    bt[0, 0], bt[1, 0] = b, a
+    rows = [dataclasses.replace(r, block_table=r.block_table.copy()) for r in w.rows]
+    rows[0].block_table[0], rows[1].block_table[0] = b, a
+    w2 = dataclasses.replace(w, rows=rows)
+    ref_o, ref_l = oracle_step(w2, T)
+    o, l = hip_step(sea, wl, w, T, meta=meta)
+    assert_attention(w2, o, l, ref_o, ref_l)
 
 
 def test_deterministic_fixed_partitions_repeat_bitwise(cuda, sea, wl):
