@@ -50,8 +50,13 @@ enum {
  * reference's is_causal argument (serving_engine/paged_attention_kernel.py:125). */
 enum {
   KVHOT_CAUSAL = 1,        /* key j is visible to query i iff j <= q_pos_offset + i */
-  KVHOT_DETERMINISTIC = 2  /* bitwise-repeatable out and lse: decode waves walk their
+  KVHOT_DETERMINISTIC = 2, /* bitwise-repeatable out and lse: decode waves walk their
                               planned key ranges in order, with no run-time sharing */
+  KVHOT_VERIFY_BLOCKS = 4  /* decode waves check the first block of their range that
+                              the launch list took from the host copy of the block
+                              table against the device table, and use the device
+                              table's (for callers that edit only the device copy);
+                              costs about 1-2% of a decode call */
 };
 
 /* Invalid-argument codes (negative return values). */
@@ -152,7 +157,8 @@ int64_t kvhot_paged_attention_workspace_bytes(
  * Launch list ("schedule") for kvhot_paged_attention, built on the host from
  * HOST copies of q_lens, k_lens, q_starts, q_pos_offsets and the block table,
  * with the head counts, head_dim, block_size, attn_flags (KVHOT_CAUSAL; the
- * KVHOT_DETERMINISTIC bit is accepted and does not change the plan) and dtype
+ * KVHOT_DETERMINISTIC and KVHOT_VERIFY_BLOCKS bits are accepted and do not
+ * change the plan) and dtype
  * the attention call will get.  The (row, kv head) key ranges of decode rows are
  * laid end to end and cut into equal numbers of 16-token slices per decode
  * work-group, one device-full of work-groups; a range cut in two becomes
@@ -160,8 +166,8 @@ int64_t kvhot_paged_attention_workspace_bytes(
  * num_decode_units range descriptors (whole work-groups: one per wave, or
  * with partition_tokens > 0 up to four per wave; each carries its row's
  * metadata and first block, so the wave's first K/V loads depend on nothing
- * else -- the kernel checks that block against the device block table before
- * using it), num_prefill_units per-work-group prefill units (longest
+ * else; with KVHOT_VERIFY_BLOCKS in the attention call's attn_flags the
+ * kernel checks that block against the device block table before using it), num_prefill_units per-work-group prefill units (longest
  * first), num_merge_units units, one per decode range cut into parts.
  * Shared prefixes: when at least 4 decode rows (with causal masking or not)
  * read the same first 256 or more keys through the same physical blocks, the

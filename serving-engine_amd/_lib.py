@@ -26,6 +26,7 @@ KVHOT_BF16 = 2
 # attn_flags bits
 KVHOT_CAUSAL = 1
 KVHOT_DETERMINISTIC = 2
+KVHOT_VERIFY_BLOCKS = 4
 
 # Split-K partials kvhot_paged_attention_noalloc holds (KVHOT_NOALLOC_SCRATCH_BYTES).
 NOALLOC_SCRATCH_BYTES = 64 << 20

@@ -87,6 +87,8 @@ struct AttnArgs {
   // in order (no claiming from other waves), so each partial sum, and with it
   // out and lse, is the same bits on every call.
   int32_t fixed;
+  // KVHOT_VERIFY_BLOCKS: decode waves check a launch list's first block.
+  int32_t verify;
 };
 
 __device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
@@ -649,7 +651,10 @@ __device__ inline int wave_max_int(int x) {
 
 // One decode work-group: launch-list work-group bx (decode descriptors at
 // sched), or without a launch list grid work-group (bx, by, bz).
-template <class TT, int D, int W>
+// MR: the launch list gives a work-group more ranges than waves (fixed
+// partitions, decode_ranges); otherwise one range per wave, and P is W.
+// VB: KVHOT_VERIFY_BLOCKS (below).
+template <class TT, int D, int W, bool MR, bool VB>
 __device__ __attribute__((always_inline)) inline void decode_wg(const AttnArgs& a, const int4* sched, int bx, int by,
                                                                 int bz) {
   extern __shared__ float smem[];
@@ -662,7 +667,7 @@ __device__ __attribute__((always_inline)) inline void decode_wg(const AttnArgs& 
   const int G = a.G;
   const int PT = a.part_tokens;
   const int S = a.dec_slots;
-  const int P = a.dec_ranges;  // ranges: wave w starts on range w (w < W <= P)
+  const int P = MR ? a.dec_ranges : W;  // ranges: wave w starts on range w (w < W <= P)
   const bool fixed = a.fixed != 0;
 
   // ---- this wave's range: slices [s0, s1) of part `part` of (row, kvh) ----
@@ -763,12 +768,23 @@ __device__ __attribute__((always_inline)) inline void decode_wg(const AttnArgs& 
   bool have = nsl > 0;     // the first slice of the range is taken without a claim
 #if KVHOT_DECODE_DEPTH < 2
   // The first slice's block comes from the launch list, built from the host
-  // copy of the block table, so that its loads wait for nothing.  The device
-  // table's entry is read before them and compared before the slice is used:
-  // a caller that edited only the device table gets the slice loaded again
-  // from the block the device table names.
-  bool check_first = sched && have && d_first >= 0;
-  const int64_t dev_first = check_first ? block_of(row, s0) : 0;
+  // copy of the block table, so that its loads wait for nothing.  With
+  // KVHOT_VERIFY_BLOCKS the device table's entry is read before them and
+  // compared before the slice is used: a caller that edited only the device
+  // table gets the slice loaded again from the block the device table names.
+  // (Off by default: waiting for that entry before the first claim cost
+  // 1-2% of a decode call.)
+  // (A buffer load: its wait is counted with the slice's vector loads, in
+  // order, rather than with LDS operations.  The check is made once, before
+  // the loop, so that nothing of it is carried through the loop.)
+  const bool check_first = VB && sched && have && d_first >= 0;
+  int dev_first = 0;
+  if (check_first) {
+    const int64_t lb = (16 * static_cast<int64_t>(s0)) / bs;
+    const __amdgpu_buffer_rsrc_t br =
+        block_rsrc(a.bt + static_cast<int64_t>(row) * a.bt_stride, static_cast<int>(4 * a.bt_stride));
+    dev_first = __builtin_amdgcn_raw_buffer_load_b32(br, static_cast<int>(4 * lb), 0, 0);
+  }
   if (have)
     wa.load_slice(a, kvh, d_first >= 0 ? min(static_cast<int64_t>(d_first), a.num_blocks - 1) : block_of(row, s0),
                   kb % bs, T);
@@ -785,6 +801,7 @@ __device__ __attribute__((always_inline)) inline void decode_wg(const AttnArgs& 
   // Ranges past the first W (launch lists of fixed partitions): wave w sets up
   // ranges w + W, w + 2W, ...; they start untouched (d[7] = 0), each with its
   // own slot, the one of the same index.
+  if constexpr (MR)
   for (int r = wave + W; r < P; r += W) {
     const int4* u = sched + 2 * (static_cast<int64_t>(bx) * P + r);
     const int4 u0 = u[0], u1 = u[1];
@@ -812,6 +829,13 @@ __device__ __attribute__((always_inline)) inline void decode_wg(const AttnArgs& 
   }
   // LDS-only barrier: the first slice's loads stay in flight across it.
   __asm__ volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+#if KVHOT_DECODE_DEPTH < 2
+  if (check_first) {
+    const int raw = __builtin_amdgcn_readfirstlane(dev_first);
+    const int64_t want = raw < 0 ? 0 : (raw >= a.num_blocks ? a.num_blocks - 1 : raw);
+    if (want != min(static_cast<int64_t>(d_first), a.num_blocks - 1)) wa.load_slice(a, kvh, want, kb % bs, T);
+  }
+#endif
 
   // Claims one slice of range v (-1 when the range is used up).
   auto claim = [&](int v) -> int {
@@ -877,11 +901,6 @@ __device__ __attribute__((always_inline)) inline void decode_wg(const AttnArgs& 
     }
     // The next slice's block id is fetched while this slice's loads land.
     const int64_t jb = j >= 0 ? block_of(__builtin_amdgcn_readfirstlane(krow), __builtin_amdgcn_readfirstlane(j)) : 0;
-    if (check_first) {
-      check_first = false;
-      const int64_t want = __builtin_amdgcn_readfirstlane(static_cast<int>(dev_first));
-      if (want != min(static_cast<int64_t>(d_first), a.num_blocks - 1)) wa.load_slice(a, kvh, want, kb % bs, T);
-    }
     if (have) {
       wa.compute_slice(a, 16 * i, kkend, INT_MAX, T);
       used = true;
@@ -906,21 +925,26 @@ __device__ __attribute__((always_inline)) inline void decode_wg(const AttnArgs& 
     if (used) flush();
     int v = -1;
     if (fixed) {
-      for (own += W; own < P; own += W)
-        if (__builtin_amdgcn_readfirstlane(dend[own] - cnt[own]) > 0) {
-          v = own;
-          break;
-        }
+      if constexpr (MR) {
+        for (own += W; own < P; own += W)
+          if (__builtin_amdgcn_readfirstlane(dend[own] - cnt[own]) > 0) {
+            v = own;
+            break;
+          }
+      }
     } else {
       v = pick(false);
     }
     if (v < 0) break;
     // The first wave to enter a range parks its state in the range's own
     // slot; a later one takes a slot from the pool (none left: it stops,
-    // and the range's other waves finish it).
+    // and the range's other waves finish it).  (One range per wave: every
+    // range was entered by its wave at the start.)
     int first = 0;
-    if (lane == 0) first = atomicExch(&info[kDecInfo * v + 7], 1) == 0 ? 1 : 0;
-    first = __builtin_amdgcn_readlane(first, 0);
+    if constexpr (MR) {
+      if (lane == 0) first = atomicExch(&info[kDecInfo * v + 7], 1) == 0 ? 1 : 0;
+      first = __builtin_amdgcn_readlane(first, 0);
+    }
     if (first) {
       slot = v;
       used = false;
@@ -1115,6 +1139,16 @@ __device__ __attribute__((always_inline)) inline void decode_wg(const AttnArgs& 
       }
     }
   };
+  if constexpr (!MR) {
+    // One range per wave: the first wave of each segment merges it.
+    if (!valid) return;
+    if (wave > 0) {
+      const int* d = info + kDecInfo * (wave - 1);
+      if (d[0] == row && d[1] == kvh && d[2] == part) return;
+    }
+    merge(row, kvh, part, nparts, pidx, qs);
+    return;
+  }
   // (Each range's description is read back from LDS rather than held in
   // registers through the loop; without a launch list the partial index is
   // recomputed, as it may not fit the table's 32 bits.)
@@ -1128,20 +1162,22 @@ __device__ __attribute__((always_inline)) inline void decode_wg(const AttnArgs& 
     const int64_t mqs = __builtin_amdgcn_readfirstlane(d[4]);
     const int64_t mpidx = sched ? static_cast<int64_t>(__builtin_amdgcn_readfirstlane(d[6]))
                                 : (static_cast<int64_t>(mrow) * a.Hkv + mkvh) * a.max_parts + mpart;
-    bool dup = false;
-    for (int r2 = 0; r2 < r; ++r2) {
-      const int* d2 = info + kDecInfo * r2;
-      dup = dup || (d2[0] == mrow && d2[1] == mkvh && d2[2] == mpart);
+    // Ranges of one segment are consecutive (the planner gives a segment's
+    // waves consecutive ranges; a range of fixed partitions is its own
+    // segment): the first of them merges.
+    if (r > 0) {
+      const int* d2 = info + kDecInfo * (r - 1);
+      if (__builtin_amdgcn_readfirstlane(static_cast<int>(d2[0] == mrow && d2[1] == mkvh && d2[2] == mpart)) != 0)
+        continue;
     }
-    if (__builtin_amdgcn_readfirstlane(static_cast<int>(dup)) != 0) continue;
     merge(mrow, mkvh, mpart, mnp, mpidx, mqs);
   }
 }
 
-template <class TT, int D, int W>
+template <class TT, int D, int W, bool MR = false, bool VB = false>
 __global__ void __launch_bounds__(64 * W)
 attn_decode_kernel(const AttnArgs a) {
-  decode_wg<TT, D, W>(a, a.sched, blockIdx.x, blockIdx.y, blockIdx.z);
+  decode_wg<TT, D, W, MR, VB>(a, a.sched, blockIdx.x, blockIdx.y, blockIdx.z);
 }
 
 // Combines the parts of split decode segments: (row, kv head) pieces that
@@ -2437,10 +2473,19 @@ static void launch_decode(const AttnArgs& a, int64_t rows, int64_t n_dec, hipStr
                              static_cast<uint32_t>(rows));
   da.dec_slots = decode_slots(W, da.dec_ranges, a.G, D);
   const size_t lds = static_cast<size_t>(decode_lds_words(da.dec_ranges, da.dec_slots, a.G, D) * 4);
-  if (lds > kMaxLdsBytes)
-    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_decode_kernel<TT, D, W>),
-                              hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
-  hipLaunchKernelGGL((attn_decode_kernel<TT, D, W>), grid, dim3(64 * W), lds, stream, da);
+  auto go = [&](auto kernel) {
+    if (lds > kMaxLdsBytes)
+      (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                static_cast<int>(lds));
+    hipLaunchKernelGGL(kernel, grid, dim3(64 * W), lds, stream, da);
+  };
+  // One instantiation per mode, so that the common one carries none of the
+  // others' code.
+  const bool mr = da.dec_ranges > W, vb = a.verify && a.sched;
+  if (mr && vb) go(attn_decode_kernel<TT, D, W, true, true>);
+  else if (mr) go(attn_decode_kernel<TT, D, W, true, false>);
+  else if (vb) go(attn_decode_kernel<TT, D, W, false, true>);
+  else go(attn_decode_kernel<TT, D, W, false, false>);
 }
 
 template <class TT, int D>
@@ -2525,7 +2570,7 @@ extern "C" int64_t kvhot_paged_attention_schedule(
       block_size <= 0 || partition_tokens < 0 || num_q_heads % num_kv_heads != 0 ||
       dtype_size(dtype) == 0 || capacity_units < 0 || bt_row_stride < 0)
     return set_error(KVHOT_EINVAL, "paged_attention_schedule: bad sizes");
-  if (attn_flags & ~(KVHOT_CAUSAL | KVHOT_DETERMINISTIC))
+  if (attn_flags & ~(KVHOT_CAUSAL | KVHOT_DETERMINISTIC | KVHOT_VERIFY_BLOCKS))
     return set_error(KVHOT_EINVAL, "paged_attention_schedule: unknown attn_flags bits");
   const bool is_causal = (attn_flags & KVHOT_CAUSAL) != 0;
   if (num_rows > 65535 || num_q_heads > 65535)
@@ -2606,7 +2651,7 @@ static int paged_attention_impl(
     return set_error(KVHOT_EINVAL, "paged_attention: bad sizes");
   if (num_q_heads % num_kv_heads != 0)
     return set_error(KVHOT_EINVAL, "paged_attention: num_q_heads % num_kv_heads != 0");
-  if (attn_flags & ~(KVHOT_CAUSAL | KVHOT_DETERMINISTIC))
+  if (attn_flags & ~(KVHOT_CAUSAL | KVHOT_DETERMINISTIC | KVHOT_VERIFY_BLOCKS))
     return set_error(KVHOT_EINVAL, "paged_attention: unknown attn_flags bits");
   if (num_rows == 0 || total_query == 0 || max_q_len == 0) return 0;
   if (!q || !k_cache || !v_cache || !out || !q_lens || !k_lens || !q_starts ||
@@ -2651,6 +2696,7 @@ static int paged_attention_impl(
   a.scale_log2 = scale * kLog2e;
   a.causal = (attn_flags & KVHOT_CAUSAL) ? 1 : 0;
   a.fixed = (attn_flags & KVHOT_DETERMINISTIC) ? 1 : 0;
+  a.verify = (attn_flags & KVHOT_VERIFY_BLOCKS) ? 1 : 0;
   a.D = static_cast<int32_t>(head_dim);
   a.total_q = total_query;
   const int64_t n_dec = schedule ? num_decode_units : 0;

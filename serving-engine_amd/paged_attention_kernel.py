@@ -101,9 +101,11 @@ def _schedule(metadata, device, hq, hkv, d, bs, pt, causal, dtype):
     return hit
 
 
-def attn_flags(is_causal: bool, deterministic: bool = False) -> int:
-    """attn_flags of the attention entry points (KVHOT_CAUSAL, KVHOT_DETERMINISTIC)."""
-    return (_lib.KVHOT_CAUSAL if is_causal else 0) | (_lib.KVHOT_DETERMINISTIC if deterministic else 0)
+def attn_flags(is_causal: bool, deterministic: bool = False, verify_block_table: bool = False) -> int:
+    """attn_flags of the attention entry points (KVHOT_CAUSAL, KVHOT_DETERMINISTIC,
+    KVHOT_VERIFY_BLOCKS)."""
+    return ((_lib.KVHOT_CAUSAL if is_causal else 0) | (_lib.KVHOT_DETERMINISTIC if deterministic else 0)
+            | (_lib.KVHOT_VERIFY_BLOCKS if verify_block_table else 0))
 
 
 def _host_max(metadata: dict, key: str, src: str) -> int:
@@ -126,7 +128,8 @@ def _check_meta(name: str, t: torch.Tensor, device: torch.device, n: int | None 
 
 
 def paged_flash_attention(q, k_cache, v_cache, metadata, num_q_heads, num_kv_heads, scale,
-                          is_causal=True, partition_tokens=None, deterministic=False):
+                          is_causal=True, partition_tokens=None, deterministic=False,
+                          verify_block_table=False):
     """Paged attention forward for a ragged batch (serving_engine/paged_attention_kernel.py:125-160).
 
     q: [total_query, num_q_heads, head_dim] (any strides with unit head_dim
@@ -139,6 +142,11 @@ def paged_flash_attention(q, k_cache, v_cache, metadata, num_q_heads, num_kv_hea
     ``deterministic=True`` makes repeated calls on the same inputs give the
     same bits (decode waves then do not share out slices at run time, which
     costs some speed), as the reference's serial key loop does.
+    ``verify_block_table=True`` makes decode waves check the first block of
+    their range, which the launch list takes from
+    ``metadata["host_block_table"]``, against ``metadata["block_table"]``
+    on the device, for callers that edit only the device copy (about 1-2%
+    of a decode call).
     """
     if q.dim() != 3 or k_cache.dim() != 4 or v_cache.dim() != 4:
         raise ValueError("expected q [T, Hq, D] and k_cache/v_cache [N, block_size, Hkv, D]")
@@ -198,7 +206,7 @@ def paged_flash_attention(q, k_cache, v_cache, metadata, num_q_heads, num_kv_hea
         q_lens.data_ptr(), metadata["k_lens"].data_ptr(),
         metadata["q_starts"].data_ptr(), metadata["q_pos_offsets"].data_ptr(),
         num_rows, total_query, max_q, max_k, num_q_heads, num_kv_heads, head_dim,
-        block_size, num_blocks, float(scale), attn_flags(is_causal, deterministic), dtype, pt,
+        block_size, num_blocks, float(scale), attn_flags(is_causal, deterministic, verify_block_table), dtype, pt,
         sched.data_ptr() if sched is not None else None, n_dec, n_pre, n_mrg, n_pfx,
         need if sched is not None else 0,
         ws.data_ptr() if ws is not None else None, ws.numel() if ws is not None else 0,

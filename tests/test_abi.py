@@ -88,7 +88,7 @@ def test_attention_rejects_bad_arguments(lib):
     bad[1] = _i64(4096, 128, 2)  # head_dim stride
     assert lib.kvhot_paged_attention(*bad) == -1
     bad = list(args)
-    bad[26] = 4  # attn_flags: only KVHOT_CAUSAL (1) and KVHOT_DETERMINISTIC (2) exist
+    bad[26] = 8  # attn_flags: only KVHOT_CAUSAL (1), KVHOT_DETERMINISTIC (2) and KVHOT_VERIFY_BLOCKS (4) exist
     assert lib.kvhot_paged_attention(*bad) == -1
     assert b"attn_flags" in lib.kvhot_last_error()
     det = list(args)

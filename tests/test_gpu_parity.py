@@ -619,9 +619,10 @@ def test_deterministic_cut_rows_repeat_bitwise(cuda, sea, wl):
 def test_device_block_table_edit_not_in_the_host_copy(cuda, sea, wl):
     """The launch list carries each decode range's first physical block from
     the host copy of the block table; a caller that then edits only the
-    device table (here: rows 0 and 1 swap their first blocks) still gets the
-    attention the device table describes, because the kernel checks that
-    block against the device table before using it."""
+    device table (here: rows 0 and 1 swap their first blocks) and passes
+    verify_block_table=True (KVHOT_VERIFY_BLOCKS) still gets the attention
+    the device table describes: the kernel checks that block against the
+    device table before using it."""
     w = wl.make_workload(2)
     announce("attention workload 2, first blocks of rows 0 and 1 swapped on the device only")
     T = wl.make_tensors(w, cuda)
@@ -634,7 +635,12 @@ def test_device_block_table_edit_not_in_the_host_copy(cuda, sea, wl):
     rows[0].block_table[0], rows[1].block_table[0] = b, a
     w2 = dataclasses.replace(w, rows=rows)
     ref_o, ref_l = oracle_step(w2, T)
-    o, l = hip_step(sea, wl, w, T, meta=meta)
+    cache = sea._PagedKVCache(T.kv_cache)
+    cache.write(T.new_k, T.new_v, 0, T.slot_mapping)
+    kc, vc = cache.blocks(0)
+    o, l = sea.paged_flash_attention(T.q, kc, vc, meta, w.num_q_heads, w.num_kv_heads,
+                                     1.0 / math.sqrt(w.head_dim), verify_block_table=True)
+    torch.cuda.synchronize()
     assert_attention(w2, o, l, ref_o, ref_l)
 
 
