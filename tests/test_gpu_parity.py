@@ -616,15 +616,18 @@ def test_deterministic_cut_rows_repeat_bitwise(cuda, sea, wl):
     assert_attention(w, o, l, ref_o, ref_l)
 
 
-def test_device_block_table_edit_not_in_the_host_copy(cuda, sea, wl):
+@pytest.mark.parametrize("pt", [None, 128])
+def test_device_block_table_edit_not_in_the_host_copy(cuda, sea, wl, pt):
     """The launch list carries each decode range's first physical block from
     the host copy of the block table; a caller that then edits only the
     device table (here: rows 0 and 1 swap their first blocks) and passes
     verify_block_table=True (KVHOT_VERIFY_BLOCKS) still gets the attention
     the device table describes: the kernel checks that block against the
-    device table before using it."""
+    device table before using it.  With 128-token partitions the decode
+    work-groups hold several ranges per wave (the other kernel
+    instantiation)."""
     w = wl.make_workload(2)
-    announce("attention workload 2, first blocks of rows 0 and 1 swapped on the device only")
+    announce(f"attention workload 2, first blocks of rows 0 and 1 swapped on the device only, partitions {pt}")
     T = wl.make_tensors(w, cuda)
     meta = wl.metadata_tensors(w, cuda)
     bt = meta["block_table"]
@@ -639,7 +642,8 @@ def test_device_block_table_edit_not_in_the_host_copy(cuda, sea, wl):
     cache.write(T.new_k, T.new_v, 0, T.slot_mapping)
     kc, vc = cache.blocks(0)
     o, l = sea.paged_flash_attention(T.q, kc, vc, meta, w.num_q_heads, w.num_kv_heads,
-                                     1.0 / math.sqrt(w.head_dim), verify_block_table=True)
+                                     1.0 / math.sqrt(w.head_dim), partition_tokens=pt,
+                                     verify_block_table=True)
     torch.cuda.synchronize()
     assert_attention(w2, o, l, ref_o, ref_l)
 
