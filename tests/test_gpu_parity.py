@@ -648,6 +648,37 @@ def test_device_block_table_edit_not_in_the_host_copy(cuda, sea, wl, pt):
     assert_attention(w2, o, l, ref_o, ref_l)
 
 
+def test_device_block_table_edit_after_a_shared_prefix(cuda, sea, wl):
+    """The same for rows that share a prefix: the 256 rows of workload 4
+    share their first 64 blocks, attended once by prefix units, and each
+    row's decode range starts at its first private block.  Rows 0 and 1 swap
+    that block on the device only; with verify_block_table=True the decode
+    ranges that fold the prefix partials in check it too."""
+    w = wl.make_workload(4)
+    announce("attention workload 4, first private blocks of rows 0 and 1 swapped on the device only")
+    T = wl.make_tensors(w, cuda)
+    meta = wl.metadata_tensors(w, cuda)
+    bt = meta["block_table"]
+    j = 64  # the first block after the 1024 shared keys
+    assert all(x.k_len > 16 * (j + 1) for x in w.rows[:2])
+    a, b = int(bt[0, j]), int(bt[1, j])
+    assert a != b and int(bt[0, 0]) == int(bt[1, 0])
+    bt[0, j], bt[1, j] = b, a
+    rows = [dataclasses.replace(r, block_table=r.block_table.copy()) for r in w.rows]
+    rows[0].block_table[j], rows[1].block_table[j] = b, a
+    w2 = dataclasses.replace(w, rows=rows)
+    ref_o, ref_l = oracle_step(w2, T)
+    cache = sea._PagedKVCache(T.kv_cache)
+    cache.write(T.new_k, T.new_v, 0, T.slot_mapping)
+    kc, vc = cache.blocks(0)
+    o, l = sea.paged_flash_attention(T.q, kc, vc, meta, w.num_q_heads, w.num_kv_heads,
+                                     1.0 / math.sqrt(w.head_dim), verify_block_table=True)
+    torch.cuda.synchronize()
+    (plan,) = [p for p in meta["_schedules"].values() if p is not None]
+    assert plan[5] > 0  # prefix units: the rows' shared blocks were grouped
+    assert_attention(w2, o, l, ref_o, ref_l)
+
+
 def test_deterministic_fixed_partitions_repeat_bitwise(cuda, sea, wl):
     """deterministic=True with fixed 128-token partitions (work-groups of
     several ranges per wave, each wave walking its own in order): two calls
